@@ -1,0 +1,335 @@
+#!/usr/bin/env python3
+"""W4A16 SwiGLU FFN benchmark on one MI355X (BASELINE.json metric: decode GB/s and prefill TFLOP/s at the
+Llama-3-8B FFN shape).
+
+Headline `value`: Llama-3-8B FFN layer decode, M = 1, fp16 activations, W4A16 group 128,
+as algorithmic GB/s (weights + x + y per layer, inputs resident in HBM). A step is one FFN layer pass over one
+batch. Six independent weight sets (553 MB) rotate so the 256 MB Infinity Cache cannot serve the weights.
+The steps are captured in a HIP graph and replayed, so host launch overhead is not timed.
+Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), the 32-layer decode stack
+(config 4), the Qwen2.5-14B g = 64 shape (config 5), a per-kernel roofline for the dominant kernel measured
+with HIP events, and the reference CPU path (restated AVX-512 GEMV) timed on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 MFMA
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def ffn_bytes(m, h, i, g):
+    """Algorithmic bytes of one FFN layer: int4 weights + 2-byte scale + 1-byte zero per group, x in, y out."""
+    w = 3 * (h * i // 2 + (h * i // g) * 3)
+    return w + m * h * 2 + m * h * 2
+
+
+def ffn_flops(m, h, i):
+    return 2 * m * h * i * 3
+
+
+def make_layers(hm, torch, dev, h, i, g, count, dtype=None, seed=0):
+    dtype = dtype or torch.float16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    layers = []
+    for _ in range(count):
+        mats = []
+        for k, n in ((h, i), (h, i), (i, h)):
+            q = torch.randint(0, 16, (k, n), dtype=torch.uint8, device=dev, generator=gen)
+            s = (torch.rand((k // g, n), device=dev, generator=gen) * 0.019 + 0.001).to(dtype)
+            z = torch.randint(0, 16, (k // g, n), dtype=torch.uint8, device=dev, generator=gen)
+            mats.append((q, s, z))
+        layers.append(hm.FfnLayer.from_logical(*mats, g, dtype=dtype))
+        del mats
+    torch.cuda.synchronize()
+    return layers
+
+
+def graph_of(torch, fn):
+    """Captures fn() (enqueueing on the current stream) into a HIP graph after one eager warm-up call."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, replays, warm_seconds=0.0, warm_replays=2):
+    """Wall time per replay (barrier + synchronize on both sides), after warm-up replays."""
+    for _ in range(warm_replays):
+        g.replay()
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + warm_seconds
+    while time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / replays
+
+
+def event_time_graph(torch, g, replays):
+    """HIP-event time per replay on the stream the graph runs on."""
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / replays
+
+
+def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0):
+    x = torch.randn((m, h), device=dev).to(layers[0].dtype)
+    y = torch.empty_like(x)
+    ws = layers[0].workspace(m)
+    sets = len(layers)
+
+    def run():
+        for L in layers:
+            L.forward(x, y, workspace=ws)
+
+    g = graph_of(torch, run)
+    replays = max(1, steps // sets)
+    sec = time_graph(torch, g, replays, warm_seconds, max(1, warmup // sets))
+    return sec / sets, g, (x, y, ws)
+
+
+def prefill_bench(hm, torch, dev, layers, m, h, steps, warmup):
+    x = torch.randn((m, h), device=dev).to(layers[0].dtype)
+    y = torch.empty_like(x)
+    ws = layers[0].workspace(m)
+    L0 = layers[0]
+
+    def run():
+        for L in layers[:2]:
+            L.forward(x, y, workspace=ws)
+
+    g = graph_of(torch, run)
+    sec = time_graph(torch, g, max(1, steps // 2), 0.0, max(1, warmup // 2))
+    del L0
+    return sec / 2
+
+
+def cpu_baseline(seconds, h, i, label):
+    """The reference CPU decode FFN (restated AVX-512 GEMV on 4352-byte tiles, bf16, M = 1) on this host."""
+    import numpy as np
+
+    from oracle import oracle as o
+
+    rng = np.random.default_rng(0)
+
+    def tiles(k, n):
+        t = (k // 128) * (n // 64)
+        a = rng.integers(0, 256, (t, 4352), dtype=np.uint8)
+        a[:, 4096:4224] = o.bf16_bits(rng.uniform(0.001, 0.02, (t, 64)).astype(np.float32)).view(np.uint8).reshape(t, 128)
+        zr = rng.integers(0, 16, (t, 8, 8), dtype=np.uint8)
+        a[:, 4224:] = np.repeat(zr, 2, axis=1).reshape(t, 128)
+        return np.ascontiguousarray(a.reshape(-1))
+
+    gate, up, down = tiles(h, i), tiles(h, i), tiles(i, h)
+    x = o.bf16_bits(rng.standard_normal(h).astype(np.float32))
+    scratch, y = np.empty(2 * i, np.uint16), np.empty(h, np.uint16)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    nbytes = ffn_bytes(1, h, i, 128)
+    results = {}
+    branch = 0
+    for th in sorted({1, threads}):
+        for _ in range(2):
+            _, branch = o.cpu_ffn_decode(x, gate, up, down, h, i, th, -1, scratch, y)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            o.cpu_ffn_decode(x, gate, up, down, h, i, th, -1, scratch, y)
+            n += 1
+            el = time.perf_counter() - t0
+            if el > seconds / 2 or n >= 2000:
+                break
+        results[th] = (el / n, n)
+    best_th = min(results, key=lambda t: results[t][0])
+    sec, n = results[best_th]
+    cpu_model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": best_th,
+        "kind": "port",
+        "sample": f"{label} FFN decode M=1 (gate, up, silu_*mul_, down GEMVs on 4352-B tiles, bf16), {n} calls after 2 warm-ups, "
+                  f"{best_th} threads ({'AVX-512' if branch else 'scalar'} branch, restated reference w4a16_gemv_cpu_fused_packed), "
+                  f"CPU {cpu_model}, {os.cpu_count()} logical CPUs visible",
+        "ms_per_call": round(sec * 1e3, 3),
+        "per_threads_ms": {str(t): round(v[0] * 1e3, 3) for t, v in results.items()},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--quick", action="store_true", help="headline decode only")
+    ap.add_argument("--sets", type=int, default=6, help="weight sets rotated per decode step")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the FFN on a single MI355X and has no multi-GPU path "
+              f"(--gpus {args.gpus} requested). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import heteromega_amd as hm
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    H, I, G = 4096, 14336, 128
+    out = {}
+
+    log("building weight sets ...")
+    layers = make_layers(hm, torch, dev, H, I, G, args.sets)
+
+    # Headline: decode M = 1.
+    sec, g1, keep = decode_bench(hm, torch, dev, layers, 1, H, args.steps, args.warmup, warm_seconds=2.0)
+    nbytes = ffn_bytes(1, H, I, G)
+    value = nbytes / sec / 1e9
+    log(f"decode M=1: {sec * 1e6:.2f} us/layer, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of HBM peak)")
+
+    # Dominant kernel: the fused gate_up + SwiGLU GEMV, timed alone with HIP events on its stream.
+    x1 = keep[0]
+    acts = torch.empty((1, I), dtype=torch.float16, device=dev)
+
+    def run_gate_up():
+        for L in layers:
+            L.gate_up(x1, acts)
+
+    g_gu = graph_of(torch, run_gate_up)
+    reps = max(4, args.steps // args.sets)
+    gu_sec = event_time_graph(torch, g_gu, reps) / args.sets
+    gu_bytes = 2 * (H * I // 2 + (H * I // G) * 3) + H * 2 + I * 2
+    achieved = gu_bytes / gu_sec / 1e9
+    out["roofline"] = {"kernel": "gemv_kernel<F16, 1, 128, fused> (gate_up + SwiGLU, M=1)", "bound": "hbm",
+                       "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                       "traffic": None, "avg_launch_us": round(gu_sec * 1e6, 3), "algorithmic_bytes_per_launch": gu_bytes}
+    log(f"gate_up kernel: {gu_sec * 1e6:.2f} us, {achieved:.1f} GB/s")
+
+    extra = {}
+    if not args.quick:
+        for m in (4, 16):
+            s, _, _ = decode_bench(hm, torch, dev, layers, m, H, args.steps, args.warmup)
+            b = ffn_bytes(m, H, I, G)
+            extra[f"decode_M{m}"] = {"us_per_layer": round(s * 1e6, 2), "GB_s": round(b / s / 1e9, 1), "frac_hbm": round(b / s / 1e9 / HBM_PEAK_GBS, 4)}
+            log(f"decode M={m}: {s * 1e6:.2f} us, {b / s / 1e9:.1f} GB/s")
+        for m in (512, 2048):
+            s = prefill_bench(hm, torch, dev, layers, m, H, max(4, args.steps // 24), 2)
+            f = ffn_flops(m, H, I)
+            extra[f"prefill_M{m}"] = {"ms_per_layer": round(s * 1e3, 3), "TFLOP_s": round(f / s / 1e12, 1),
+                                       "frac_mfma": round(f / s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+            log(f"prefill M={m}: {s * 1e3:.3f} ms, {f / s / 1e12:.1f} TFLOP/s")
+    del layers, g1, g_gu, keep
+    torch.cuda.empty_cache()
+
+    if not args.quick:
+        # 32 distinct layers, RMSNorm (eps 1e-5) + residual between layers, decode M = 1.
+        stack = make_layers(hm, torch, dev, H, I, G, 32, seed=1)
+        x = torch.randn((1, H), device=dev).to(torch.float16)
+        normed, y = torch.empty_like(x), torch.empty_like(x)
+        ones = torch.ones(H, dtype=torch.float16, device=dev)
+        ws = stack[0].workspace(1)
+
+        def token():
+            hm.rmsnorm(normed, x, ones, 1e-5)
+            for li, L in enumerate(stack):
+                L.forward(normed, y, workspace=ws)
+                if li + 1 < len(stack):
+                    hm.residual_rmsnorm(x, y, ones, normed, 1e-5)
+                else:
+                    hm.residual_add2(x, y)
+
+        gt = graph_of(torch, token)
+        tok = time_graph(torch, gt, 128, 0.5, 4)
+        sb = 32 * ffn_bytes(1, H, I, G)
+        extra["stack32_decode"] = {"us_per_token": round(tok * 1e6, 1), "ms_per_128_tokens": round(128 * tok * 1e3, 2),
+                                   "GB_s": round(sb / tok / 1e9, 1), "frac_hbm": round(sb / tok / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"32-layer stack: {tok * 1e6:.1f} us/token")
+        del stack, gt
+        torch.cuda.empty_cache()
+
+        # Qwen2.5-14B FFN shape, group 64.
+        qh, qi, qg = 5120, 13824, 64
+        ql = make_layers(hm, torch, dev, qh, qi, qg, 4, seed=2)
+        s, _, _ = decode_bench(hm, torch, dev, ql, 1, qh, args.steps, args.warmup)
+        b = ffn_bytes(1, qh, qi, qg)
+        extra["qwen14b_g64_decode_M1"] = {"us_per_layer": round(s * 1e6, 2), "GB_s": round(b / s / 1e9, 1), "frac_hbm": round(b / s / 1e9 / HBM_PEAK_GBS, 4)}
+        s = prefill_bench(hm, torch, dev, ql, 1024, qh, max(4, args.steps // 24), 2)
+        f = ffn_flops(1024, qh, qi)
+        extra["qwen14b_g64_prefill_M1024"] = {"ms_per_layer": round(s * 1e3, 3), "TFLOP_s": round(f / s / 1e12, 1),
+                                               "frac_mfma": round(f / s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+        log(f"qwen decode {extra['qwen14b_g64_decode_M1']}, prefill {extra['qwen14b_g64_prefill_M1024']}")
+        del ql
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline ...")
+        cpu = cpu_baseline(args.cpu_seconds, H, I, "Llama-3-8B")
+        log(f"CPU: {cpu['value']} GB/s with {cpu['cores']} threads")
+        c1 = cpu_baseline(min(6.0, args.cpu_seconds / 2), 2048, 8192, "Llama-3.2-1B")
+        cpu["config1_llama32_1b"] = {"GB_s": c1["value"], "threads": c1["cores"], "ms_per_call": c1["ms_per_call"]}
+
+    line = {
+        "metric": "W4A16 FFN decode GB/s (%HBM peak) + prefill TFLOP/s, Llama-3-8B FFN shape",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded random W4A16 weights, N(0,1) activations)",
+        "config": {"workload": "Llama-3-8B SwiGLU FFN layer decode, M=1, H=4096, I=14336, W4A16 group 128, fp16 activations",
+                   "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4), "weight_sets_rotated": args.sets,
+                   "bytes_per_step": nbytes, "timing": "HIP graph replay, wall clock with synchronize on both sides"},
+        "roofline": out["roofline"],
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,697 @@
+// C ABI of the W4A16 FFN engine (include/hm_w4a16.h): validation, allocation at create time, dispatch.
+#include "../../include/hm_w4a16.h"
+#include "hm_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+struct hm_weights {
+    hm::Planes p;
+    void *buffer = nullptr;
+    int64_t bytes = 0;
+    int64_t quant_bytes = 0, meta_bytes = 0;
+};
+
+struct hm_ffn {
+    hm_weights gate_up; // [H, 2 I], strips alternate gate / up per 16 channels
+    hm_weights down;    // [I, H]
+    int64_t hidden = 0, inter = 0;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+hm_status fail(hm_status s, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return s;
+}
+
+hm_status hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorOutOfMemory ? HM_OUT_OF_MEMORY : HM_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+bool valid_group(int64_t g) { return g == 32 || g == 64 || g == 128; }
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Allocates both planes of a K x N matrix in one device buffer.
+hm_status alloc_planes(hm_weights *w, int64_t K, int64_t N, int64_t group, int dtype) {
+    w->p.K = K;
+    w->p.N = N;
+    w->p.group = group;
+    w->p.dtype = dtype;
+    w->quant_bytes = K * N / 2;
+    w->meta_bytes = (N / 16) * (K / group) * 16 * 4;
+    const int64_t meta_off = round_up(w->quant_bytes, 256);
+    w->bytes = meta_off + w->meta_bytes;
+    const hipError_t e = hipMalloc(&w->buffer, static_cast<size_t>(w->bytes));
+    if (e != hipSuccess) {
+        w->buffer = nullptr;
+        return hip_fail(e, "hipMalloc of the repacked weights");
+    }
+    w->p.quant = static_cast<const uint8_t *>(w->buffer);
+    w->p.meta = reinterpret_cast<const uint32_t *>(static_cast<uint8_t *>(w->buffer) + meta_off);
+    return HM_OK;
+}
+
+void free_planes(hm_weights *w) {
+    if (w->buffer != nullptr) {
+        (void)hipFree(w->buffer);
+        w->buffer = nullptr;
+    }
+}
+
+hm_status check_dtype(hm_dtype dtype) {
+    if (dtype != HM_BF16 && dtype != HM_FP16) {
+        return fail(HM_INVALID_ARGUMENT, "dtype must be HM_BF16 or HM_FP16, got %d", static_cast<int>(dtype));
+    }
+    return HM_OK;
+}
+
+hm_status check_tile_source(const uint8_t *tiles, int64_t packed_k, int64_t packed_n, int64_t K, int64_t N, const char *what) {
+    if (tiles == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "%s: null packed matrix", what);
+    }
+    if (packed_k <= 0 || packed_n <= 0 || packed_k % 128 || packed_n % 64) {
+        return fail(HM_INVALID_ARGUMENT, "%s: packed matrix [%lld, %lld] must be multiples of 128 x 64", what,
+                    static_cast<long long>(packed_k), static_cast<long long>(packed_n));
+    }
+    if (K <= 0 || N <= 0 || K % 128 || N % 16 || K > packed_k || N > packed_n) {
+        return fail(HM_INVALID_ARGUMENT, "%s: block [%lld, %lld] must be multiples of 128 x 16 inside [%lld, %lld]", what,
+                    static_cast<long long>(K), static_cast<long long>(N), static_cast<long long>(packed_k),
+                    static_cast<long long>(packed_n));
+    }
+    return HM_OK;
+}
+
+hm_status check_logical(const uint8_t *q, const uint16_t *s, const uint8_t *z, int64_t K, int64_t N, int64_t group,
+                        const char *what) {
+    if (q == nullptr || s == nullptr || z == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "%s: null tensor", what);
+    }
+    if (!valid_group(group)) {
+        return fail(HM_INVALID_ARGUMENT, "%s: group must be 32, 64 or 128, got %lld", what, static_cast<long long>(group));
+    }
+    if (K <= 0 || N <= 0 || K % 128 || N % 16) {
+        return fail(HM_INVALID_ARGUMENT, "%s: [%lld, %lld] must be multiples of 128 x 16", what, static_cast<long long>(K),
+                    static_cast<long long>(N));
+    }
+    return HM_OK;
+}
+
+// Rows beyond this use the MFMA GEMM; up to it, the decode GEMV.
+constexpr int64_t kGemvMaxRows = 16;
+
+int gemv_waves(int64_t kt_count, bool fused) {
+    if (fused) {
+        return 4;
+    }
+    return kt_count >= 32 ? 8 : 4;
+}
+
+hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t strip_begin,
+                     int64_t n, int64_t kt_begin, int64_t kt_count, bool fused, void *workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+    if (M <= kGemvMaxRows) {
+        hm::GemvCall c;
+        c.w = p;
+        c.x = static_cast<const uint16_t *>(x);
+        c.ldx = ldx;
+        c.y = static_cast<uint16_t *>(y);
+        c.ldy = ldy;
+        c.m = M;
+        c.strip_begin = strip_begin;
+        c.n = n;
+        c.kt_begin = kt_begin;
+        c.kt_count = kt_count;
+        c.fused = fused;
+        c.waves = gemv_waves(kt_count, fused);
+        c.splits = hm::gemv_pick_splits(c);
+        const size_t need = hm::gemv_partial_bytes(c);
+        if (need > workspace_bytes) {
+            return fail(HM_WORKSPACE_TOO_SMALL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+        }
+        c.partial = static_cast<float *>(workspace);
+        const hipError_t e = hm::launch_gemv(c, stream);
+        return e == hipSuccess ? HM_OK : hip_fail(e, "gemv launch");
+    }
+    const int64_t cols = fused ? 2 * n : n;
+    if (cols % 128) {
+        return fail(HM_UNSUPPORTED, "GEMM path (M > %lld) needs %s a multiple of %d, got %lld", static_cast<long long>(kGemvMaxRows),
+                    fused ? "channels" : "n", fused ? 64 : 128, static_cast<long long>(n));
+    }
+    hm::GemmCall c;
+    c.w = p;
+    c.x = static_cast<const uint16_t *>(x);
+    c.ldx = ldx;
+    c.y = static_cast<uint16_t *>(y);
+    c.ldy = ldy;
+    c.m = M;
+    c.strip_begin = strip_begin;
+    c.n = n;
+    c.kt_begin = kt_begin;
+    c.kt_count = kt_count;
+    c.fused = fused;
+    const hipError_t e = hm::launch_gemm(c, stream);
+    return e == hipSuccess ? HM_OK : hip_fail(e, "gemm launch");
+}
+
+size_t linear_workspace(const hm::Planes &p, int64_t M, int64_t n, int64_t kt_count, bool fused) {
+    if (M > kGemvMaxRows) {
+        return 0;
+    }
+    hm::GemvCall c;
+    c.w = p;
+    c.m = M;
+    c.n = n;
+    c.kt_count = kt_count;
+    c.fused = fused;
+    c.waves = gemv_waves(kt_count, fused);
+    return hm::gemv_partial_bytes(c);
+}
+
+hm_status check_activation(const void *x, int64_t ldx, int64_t width, const char *what) {
+    if (x == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "%s: null pointer", what);
+    }
+    if (!aligned(x, 16) || ldx % 8 || ldx < width) {
+        return fail(HM_INVALID_ARGUMENT, "%s: needs 16-byte alignment and a leading dimension that is a multiple of 8 and >= %lld (got %lld)",
+                    what, static_cast<long long>(width), static_cast<long long>(ldx));
+    }
+    return HM_OK;
+}
+
+hm_status check_output(const void *y, int64_t ldy, int64_t width, const char *what) {
+    if (y == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "%s: null pointer", what);
+    }
+    if (!aligned(y, 2) || ldy < width) {
+        return fail(HM_INVALID_ARGUMENT, "%s: leading dimension %lld < %lld", what, static_cast<long long>(ldy), static_cast<long long>(width));
+    }
+    return HM_OK;
+}
+
+hm_status check_channels(const hm_ffn *f, int64_t b, int64_t e) {
+    if (b < 0 || b >= e || e > f->inter || b % 128 || e % 128) {
+        return fail(HM_INVALID_ARGUMENT, "channel range [%lld, %lld) must be a nonempty range of multiples of 128 inside [0, %lld)",
+                    static_cast<long long>(b), static_cast<long long>(e), static_cast<long long>(f->inter));
+    }
+    return HM_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int hm_abi_version(void) { return HM_ABI_VERSION; }
+
+const char *hm_last_error(void) { return g_error.c_str(); }
+
+int64_t hm_packed_bytes(int64_t K, int64_t N) {
+    if (K <= 0 || N <= 0 || K % 128 || N % 64) {
+        return -1;
+    }
+    return (K / 128) * (N / 64) * 4352;
+}
+
+int64_t hm_packed_tile_index(int64_t c, int64_t r, int64_t tiles_k, int64_t tiles_n) {
+    if (tiles_k <= 0 || tiles_n <= 0 || c < 0 || c >= tiles_n || r < 0 || r >= tiles_k) {
+        return -1;
+    }
+    int64_t before = c / 8;
+    for (int64_t g = 0; g < c % 8; ++g) {
+        before += (tiles_n - g + 7) / 8;
+    }
+    return before * tiles_k + r;
+}
+
+hm_status hm_pack_w4a16(const uint8_t *q, const uint16_t *scales, const int8_t *zeros, int64_t K, int64_t N, uint8_t *out) {
+    if (q == nullptr || scales == nullptr || zeros == nullptr || out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_pack_w4a16: null pointer");
+    }
+    if (K <= 0 || N <= 0 || K % 128 || N % 64) {
+        return fail(HM_INVALID_ARGUMENT, "hm_pack_w4a16: K must be a multiple of 128 and N of 64, got %lldx%lld",
+                    static_cast<long long>(K), static_cast<long long>(N));
+    }
+    const int64_t tiles_k = K / 128, tiles_n = N / 64;
+    for (int64_t c = 0; c < tiles_n; ++c) {
+        for (int64_t r = 0; r < tiles_k; ++r) {
+            uint8_t *tile = out + hm_packed_tile_index(c, r, tiles_k, tiles_n) * 4352;
+            // Byte ((a * 8 + cc) * 8 + b) * 4 + j: row 8 a + b, columns 8 cc + 2 j (low) and + 1 (high).
+            for (int byte = 0; byte < 4096; ++byte) {
+                const int j = byte & 3, b = (byte >> 2) & 7, cc = (byte >> 5) & 7, a = byte >> 8;
+                const uint8_t *row = q + (r * 128 + a * 8 + b) * N + c * 64 + cc * 8 + 2 * j;
+                tile[byte] = static_cast<uint8_t>((row[0] & 0x0F) | ((row[1] & 0x0F) << 4));
+            }
+            std::memcpy(tile + 4096, scales + r * N + c * 64, 128);
+            for (int i = 0; i < 64; ++i) {
+                const uint8_t z = static_cast<uint8_t>(zeros[r * N + c * 64 + i]);
+                tile[4224 + (i >> 3) * 16 + (i & 7)] = z;
+                tile[4224 + (i >> 3) * 16 + 8 + (i & 7)] = z;
+            }
+        }
+    }
+    return HM_OK;
+}
+
+hm_status hm_awq_unpack(const int32_t *packed, int64_t rows, int64_t cols8, uint8_t *out) {
+    if (packed == nullptr || out == nullptr || rows <= 0 || cols8 <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_awq_unpack: bad arguments");
+    }
+    static const int order[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t j = 0; j < cols8; ++j) {
+            const uint32_t v = static_cast<uint32_t>(packed[r * cols8 + j]);
+            for (int k = 0; k < 8; ++k) {
+                out[r * cols8 * 8 + 8 * j + k] = static_cast<uint8_t>((v >> (4 * order[k])) & 0xFu);
+            }
+        }
+    }
+    return HM_OK;
+}
+
+hm_status hm_weights_from_tiles(const uint8_t *tiles, int64_t packed_k, int64_t packed_n, int64_t K, int64_t N, hm_dtype dtype,
+                                void *stream, hm_weights **out) {
+    if (out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_from_tiles: null output handle");
+    }
+    *out = nullptr;
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK || (st = check_tile_source(tiles, packed_k, packed_n, K, N, "hm_weights_from_tiles")) != HM_OK) {
+        return st;
+    }
+    auto *w = new hm_weights;
+    if ((st = alloc_planes(w, K, N, 128, dtype)) != HM_OK) {
+        delete w;
+        return st;
+    }
+    hm::TileSource src;
+    src.tiles = tiles;
+    src.tiles_k = packed_k / 128;
+    src.tiles_n = packed_n / 64;
+    const hipError_t e = hm::launch_repack_tiles(&src, 1, false, const_cast<uint8_t *>(w->p.quant), const_cast<uint32_t *>(w->p.meta), K,
+                                                 N, dtype, as_stream(stream));
+    if (e != hipSuccess) {
+        free_planes(w);
+        delete w;
+        return hip_fail(e, "repack launch");
+    }
+    *out = w;
+    return HM_OK;
+}
+
+hm_status hm_weights_from_logical(const uint8_t *q, const uint16_t *scales, const uint8_t *zeros, int64_t K, int64_t N, int64_t group,
+                                  hm_dtype dtype, void *stream, hm_weights **out) {
+    if (out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_from_logical: null output handle");
+    }
+    *out = nullptr;
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK || (st = check_logical(q, scales, zeros, K, N, group, "hm_weights_from_logical")) != HM_OK) {
+        return st;
+    }
+    auto *w = new hm_weights;
+    if ((st = alloc_planes(w, K, N, group, dtype)) != HM_OK) {
+        delete w;
+        return st;
+    }
+    hm::LogicalSource src;
+    src.q = q;
+    src.scales = scales;
+    src.zeros = zeros;
+    src.ld = N;
+    const hipError_t e = hm::launch_repack_logical(&src, 1, false, const_cast<uint8_t *>(w->p.quant), const_cast<uint32_t *>(w->p.meta), K,
+                                                   N, group, as_stream(stream));
+    if (e != hipSuccess) {
+        free_planes(w);
+        delete w;
+        return hip_fail(e, "repack launch");
+    }
+    *out = w;
+    return HM_OK;
+}
+
+hm_status hm_weights_to_logical(const hm_weights *w, uint8_t *q, uint16_t *scales, uint8_t *zeros, void *stream) {
+    if (w == nullptr || q == nullptr || scales == nullptr || zeros == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_to_logical: null pointer");
+    }
+    const hipError_t e = hm::launch_unpack(w->p, q, scales, zeros, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "unpack launch");
+}
+
+hm_status hm_weights_info(const hm_weights *w, int64_t *K, int64_t *N, int64_t *group, int32_t *dtype, int64_t *device_bytes) {
+    if (w == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_info: null handle");
+    }
+    if (K) *K = w->p.K;
+    if (N) *N = w->p.N;
+    if (group) *group = w->p.group;
+    if (dtype) *dtype = w->p.dtype;
+    if (device_bytes) *device_bytes = w->bytes;
+    return HM_OK;
+}
+
+hm_status hm_weights_planes(const hm_weights *w, const void **quant, int64_t *quant_bytes, const void **meta, int64_t *meta_bytes) {
+    if (w == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_planes: null handle");
+    }
+    if (quant) *quant = w->p.quant;
+    if (quant_bytes) *quant_bytes = w->quant_bytes;
+    if (meta) *meta = w->p.meta;
+    if (meta_bytes) *meta_bytes = w->meta_bytes;
+    return HM_OK;
+}
+
+hm_status hm_weights_destroy(hm_weights *w) {
+    if (w != nullptr) {
+        free_planes(w);
+        delete w;
+    }
+    return HM_OK;
+}
+
+size_t hm_linear_workspace_bytes(const hm_weights *w, int64_t M, int64_t k, int64_t n) {
+    if (w == nullptr || M <= 0 || k <= 0 || n <= 0) {
+        return 0;
+    }
+    return linear_workspace(w->p, M, n, k / 128, false);
+}
+
+hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t k, int64_t n, int64_t col_begin,
+                    void *workspace, size_t workspace_bytes, void *stream) {
+    if (w == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_linear: null weights");
+    }
+    if (M <= 0 || k <= 0 || n <= 0 || k % 128 || n % 16 || col_begin < 0 || col_begin % 16 || k > w->p.K || col_begin + n > w->p.N) {
+        return fail(HM_INVALID_ARGUMENT, "hm_linear: block k=%lld, columns [%lld, %lld) must be multiples of 128 / 16 inside [%lld, %lld]",
+                    static_cast<long long>(k), static_cast<long long>(col_begin), static_cast<long long>(col_begin + n),
+                    static_cast<long long>(w->p.K), static_cast<long long>(w->p.N));
+    }
+    hm_status st = check_activation(x, ldx, k, "hm_linear x");
+    if (st != HM_OK || (st = check_output(y, ldy, n, "hm_linear y")) != HM_OK) {
+        return st;
+    }
+    return run_linear(w->p, y, ldy, x, ldx, M, col_begin / 16, n, 0, k / 128, false, workspace, workspace_bytes, as_stream(stream));
+}
+
+hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden, int64_t inter, hm_dtype dtype,
+                            void *stream, hm_ffn **out) {
+    if (out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_from_tiles: null output handle");
+    }
+    *out = nullptr;
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    if (hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_from_tiles: hidden and inter must be positive multiples of 128, got %lld, %lld",
+                    static_cast<long long>(hidden), static_cast<long long>(inter));
+    }
+    if ((st = check_tile_source(gate, hidden, inter, hidden, inter, "gate")) != HM_OK ||
+        (st = check_tile_source(up, hidden, inter, hidden, inter, "up")) != HM_OK ||
+        (st = check_tile_source(down, inter, hidden, inter, hidden, "down")) != HM_OK) {
+        return st;
+    }
+    auto *f = new hm_ffn;
+    f->hidden = hidden;
+    f->inter = inter;
+    if ((st = alloc_planes(&f->gate_up, hidden, 2 * inter, 128, dtype)) != HM_OK) {
+        delete f;
+        return st;
+    }
+    if ((st = alloc_planes(&f->down, inter, hidden, 128, dtype)) != HM_OK) {
+        free_planes(&f->gate_up);
+        delete f;
+        return st;
+    }
+    hm::TileSource gu[2];
+    gu[0].tiles = gate;
+    gu[1].tiles = up;
+    gu[0].tiles_k = gu[1].tiles_k = hidden / 128;
+    gu[0].tiles_n = gu[1].tiles_n = inter / 64;
+    hm::TileSource d;
+    d.tiles = down;
+    d.tiles_k = inter / 128;
+    d.tiles_n = hidden / 64;
+    hipError_t e = hm::launch_repack_tiles(gu, 2, true, const_cast<uint8_t *>(f->gate_up.p.quant), const_cast<uint32_t *>(f->gate_up.p.meta),
+                                           hidden, 2 * inter, dtype, as_stream(stream));
+    if (e == hipSuccess) {
+        e = hm::launch_repack_tiles(&d, 1, false, const_cast<uint8_t *>(f->down.p.quant), const_cast<uint32_t *>(f->down.p.meta), inter,
+                                    hidden, dtype, as_stream(stream));
+    }
+    if (e != hipSuccess) {
+        free_planes(&f->gate_up);
+        free_planes(&f->down);
+        delete f;
+        return hip_fail(e, "repack launch");
+    }
+    *out = f;
+    return HM_OK;
+}
+
+hm_status hm_ffn_from_logical(const uint8_t *gate_q, const uint16_t *gate_s, const uint8_t *gate_z, const uint8_t *up_q, const uint16_t *up_s,
+                              const uint8_t *up_z, const uint8_t *down_q, const uint16_t *down_s, const uint8_t *down_z, int64_t hidden,
+                              int64_t inter, int64_t group, hm_dtype dtype, void *stream, hm_ffn **out) {
+    if (out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_from_logical: null output handle");
+    }
+    *out = nullptr;
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK || (st = check_logical(gate_q, gate_s, gate_z, hidden, inter, group, "gate")) != HM_OK ||
+        (st = check_logical(up_q, up_s, up_z, hidden, inter, group, "up")) != HM_OK ||
+        (st = check_logical(down_q, down_s, down_z, inter, hidden, group, "down")) != HM_OK) {
+        return st;
+    }
+    auto *f = new hm_ffn;
+    f->hidden = hidden;
+    f->inter = inter;
+    if ((st = alloc_planes(&f->gate_up, hidden, 2 * inter, group, dtype)) != HM_OK) {
+        delete f;
+        return st;
+    }
+    if ((st = alloc_planes(&f->down, inter, hidden, group, dtype)) != HM_OK) {
+        free_planes(&f->gate_up);
+        delete f;
+        return st;
+    }
+    hm::LogicalSource gu[2];
+    gu[0].q = gate_q;
+    gu[0].scales = gate_s;
+    gu[0].zeros = gate_z;
+    gu[1].q = up_q;
+    gu[1].scales = up_s;
+    gu[1].zeros = up_z;
+    gu[0].ld = gu[1].ld = inter;
+    hm::LogicalSource d;
+    d.q = down_q;
+    d.scales = down_s;
+    d.zeros = down_z;
+    d.ld = hidden;
+    hipError_t e = hm::launch_repack_logical(gu, 2, true, const_cast<uint8_t *>(f->gate_up.p.quant),
+                                             const_cast<uint32_t *>(f->gate_up.p.meta), hidden, 2 * inter, group, as_stream(stream));
+    if (e == hipSuccess) {
+        e = hm::launch_repack_logical(&d, 1, false, const_cast<uint8_t *>(f->down.p.quant), const_cast<uint32_t *>(f->down.p.meta), inter,
+                                      hidden, group, as_stream(stream));
+    }
+    if (e != hipSuccess) {
+        free_planes(&f->gate_up);
+        free_planes(&f->down);
+        delete f;
+        return hip_fail(e, "repack launch");
+    }
+    *out = f;
+    return HM_OK;
+}
+
+hm_status hm_ffn_info(const hm_ffn *f, int64_t *hidden, int64_t *inter, int64_t *group, int32_t *dtype) {
+    if (f == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_info: null handle");
+    }
+    if (hidden) *hidden = f->hidden;
+    if (inter) *inter = f->inter;
+    if (group) *group = f->down.p.group;
+    if (dtype) *dtype = f->down.p.dtype;
+    return HM_OK;
+}
+
+hm_status hm_ffn_destroy(hm_ffn *f) {
+    if (f != nullptr) {
+        free_planes(&f->gate_up);
+        free_planes(&f->down);
+        delete f;
+    }
+    return HM_OK;
+}
+
+size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
+    if (f == nullptr || max_m <= 0) {
+        return 0;
+    }
+    const size_t act = static_cast<size_t>(round_up(max_m * f->inter * 2, 256));
+    size_t partial = 0;
+    for (int64_t m = 1; m <= std::min<int64_t>(max_m, kGemvMaxRows); ++m) {
+        partial = std::max(partial, linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false));
+    }
+    return act + partial;
+}
+
+hm_status hm_ffn_gate_up(const hm_ffn *f, void *act, int64_t ld_act, const void *x, int64_t ldx, int64_t M, int64_t ch_begin, int64_t ch_end,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    if (f == nullptr || M <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_gate_up: null handle or M <= 0");
+    }
+    hm_status st = check_channels(f, ch_begin, ch_end);
+    if (st != HM_OK || (st = check_activation(x, ldx, f->hidden, "hm_ffn_gate_up x")) != HM_OK ||
+        (st = check_output(act, ld_act, ch_end - ch_begin, "hm_ffn_gate_up act")) != HM_OK) {
+        return st;
+    }
+    return run_linear(f->gate_up.p, act, ld_act, x, ldx, M, 2 * (ch_begin / 16), ch_end - ch_begin, 0, f->hidden / 128, true, workspace,
+                      workspace_bytes, as_stream(stream));
+}
+
+hm_status hm_ffn_down(const hm_ffn *f, void *y, int64_t ldy, const void *act, int64_t ld_act, int64_t M, int64_t ch_begin, int64_t ch_end,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+    if (f == nullptr || M <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_down: null handle or M <= 0");
+    }
+    hm_status st = check_channels(f, ch_begin, ch_end);
+    if (st != HM_OK || (st = check_activation(act, ld_act, ch_end - ch_begin, "hm_ffn_down act")) != HM_OK ||
+        (st = check_output(y, ldy, f->hidden, "hm_ffn_down y")) != HM_OK) {
+        return st;
+    }
+    return run_linear(f->down.p, y, ldy, act, ld_act, M, 0, f->hidden, ch_begin / 128, (ch_end - ch_begin) / 128, false, workspace,
+                      workspace_bytes, as_stream(stream));
+}
+
+hm_status hm_ffn_forward(const hm_ffn *f, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t ch_begin, int64_t ch_end,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    if (f == nullptr || M <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_forward: null handle or M <= 0");
+    }
+    hm_status st = check_channels(f, ch_begin, ch_end);
+    if (st != HM_OK) {
+        return st;
+    }
+    const size_t need = hm_ffn_workspace_bytes(f, M);
+    if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)) {
+        return fail(HM_WORKSPACE_TOO_SMALL, "hm_ffn_forward: workspace must be 256-byte aligned with >= %zu bytes (got %zu)", need,
+                    workspace_bytes);
+    }
+    const int64_t n = ch_end - ch_begin;
+    const size_t act_bytes = static_cast<size_t>(round_up(M * f->inter * 2, 256));
+    void *act = workspace;
+    void *rest = static_cast<uint8_t *>(workspace) + act_bytes;
+    const size_t rest_bytes = workspace_bytes - act_bytes;
+    if ((st = hm_ffn_gate_up(f, act, n, x, ldx, M, ch_begin, ch_end, rest, rest_bytes, stream)) != HM_OK) {
+        return st;
+    }
+    return hm_ffn_down(f, y, ldy, act, n, M, ch_begin, ch_end, rest, rest_bytes, stream);
+}
+
+hm_status hm_silu_mul(const void *gate_up, int64_t ld_in, void *act, int64_t ld_out, int64_t rows, int64_t n, int32_t layout, hm_dtype dtype,
+                      void *stream) {
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    const bool inter = layout == HM_GATE_UP_INTERLEAVED;
+    if (gate_up == nullptr || act == nullptr || rows < 0 || n <= 0 || n % (inter ? 64 : 8) || ld_in % 8 || ld_out % 8 || ld_in < 2 * n ||
+        ld_out < n || !aligned(gate_up, 16) || !aligned(act, 16) || (layout != HM_GATE_UP_BLOCKED && !inter)) {
+        return fail(HM_INVALID_ARGUMENT, "hm_silu_mul: gate_up [rows, 2n] and act [rows, n] must be 16-byte aligned, n a multiple of %d",
+                    inter ? 64 : 8);
+    }
+    const hipError_t e = hm::launch_silu_mul(static_cast<const uint16_t *>(gate_up), ld_in, static_cast<uint16_t *>(act), ld_out, rows, n,
+                                             inter, dtype, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "silu_mul launch");
+}
+
+hm_status hm_rmsnorm(void *out, int64_t ld_out, const void *x, int64_t ldx, const void *weight, int64_t rows, int64_t cols, float eps, hm_dtype dtype,
+                     void *stream) {
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    if (out == nullptr || x == nullptr || weight == nullptr || rows < 0 || cols <= 0 || cols % 8 || ld_out % 8 || ldx % 8 || ldx < cols ||
+        ld_out < cols || !aligned(out, 16) || !aligned(x, 16) || !aligned(weight, 16) || !(eps >= 0.0f)) {
+        return fail(HM_INVALID_ARGUMENT, "hm_rmsnorm: rows of a multiple of 8 columns, 16-byte aligned, eps >= 0");
+    }
+    const hipError_t e = hm::launch_rmsnorm(static_cast<uint16_t *>(out), ld_out, static_cast<const uint16_t *>(x), ldx,
+                                            static_cast<const uint16_t *>(weight), rows, cols, eps, dtype, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "rmsnorm launch");
+}
+
+hm_status hm_residual_add2(void *x, int64_t ldx, const void *a, int64_t lda, const void *b, int64_t ldb, int64_t rows, int64_t cols,
+                           hm_dtype dtype, void *stream) {
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    if (x == nullptr || rows < 0 || cols <= 0 || cols % 8 || ldx % 8 || ldx < cols || !aligned(x, 16) ||
+        (a != nullptr && (lda % 8 || lda < cols || !aligned(a, 16))) || (b != nullptr && (ldb % 8 || ldb < cols || !aligned(b, 16)))) {
+        return fail(HM_INVALID_ARGUMENT, "hm_residual_add2: rows of a multiple of 8 columns, 16-byte aligned");
+    }
+    const hipError_t e = hm::launch_residual_add2(static_cast<uint16_t *>(x), ldx, static_cast<const uint16_t *>(a), lda,
+                                                  static_cast<const uint16_t *>(b), ldb, rows, cols, dtype, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "residual_add2 launch");
+}
+
+hm_status hm_residual_rmsnorm(void *x, int64_t ldx, const void *y, int64_t ldy, const void *weight, void *normed, int64_t ld_normed, int64_t rows,
+                              int64_t cols, float eps, hm_dtype dtype, void *stream) {
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    if (x == nullptr || y == nullptr || weight == nullptr || normed == nullptr || rows < 0 || cols <= 0 || cols % 8 || ldx % 8 || ldy % 8 ||
+        ld_normed % 8 || ldx < cols || ldy < cols || ld_normed < cols || !aligned(x, 16) || !aligned(y, 16) || !aligned(weight, 16) ||
+        !aligned(normed, 16) || !(eps >= 0.0f)) {
+        return fail(HM_INVALID_ARGUMENT, "hm_residual_rmsnorm: rows of a multiple of 8 columns, 16-byte aligned, eps >= 0");
+    }
+    const hipError_t e = hm::launch_residual_rmsnorm(static_cast<uint16_t *>(x), ldx, static_cast<const uint16_t *>(y), ldy,
+                                                     static_cast<const uint16_t *>(weight), static_cast<uint16_t *>(normed), ld_normed, rows,
+                                                     cols, eps, dtype, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "residual_rmsnorm launch");
+}
+
+hm_status hm_partition_check(int64_t intermediate, int64_t npu_channels, int64_t alignment) {
+    if (intermediate <= 0 || alignment <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "partition: intermediate_channels and alignment must be positive integers");
+    }
+    if (npu_channels < 0 || npu_channels > intermediate) {
+        return fail(HM_INVALID_ARGUMENT, "partition: npu_channels must lie within the FFN width");
+    }
+    if (intermediate % alignment || npu_channels % alignment) {
+        return fail(HM_INVALID_ARGUMENT, "partition: FFN width and NPU channel count must satisfy alignment");
+    }
+    return HM_OK;
+}
+
+hm_status hm_partition_from_ratio(int64_t intermediate, double npu_ratio, int64_t alignment, int64_t *npu_channels) {
+    if (npu_channels == nullptr || intermediate <= 0 || alignment <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "partition: intermediate_channels and alignment must be positive integers");
+    }
+    if (!std::isfinite(npu_ratio) || npu_ratio < 0.0 || npu_ratio > 1.0) {
+        return fail(HM_INVALID_ARGUMENT, "partition: npu_ratio must be finite and in [0, 1]");
+    }
+    const double units = static_cast<double>(intermediate) * npu_ratio / static_cast<double>(alignment);
+    *npu_channels = static_cast<int64_t>(std::floor(units + 0.5)) * alignment;
+    return hm_partition_check(intermediate, *npu_channels, alignment);
+}
+
+} // extern "C"

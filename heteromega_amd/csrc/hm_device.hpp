@@ -1,0 +1,111 @@
+// Device helpers shared by the gfx950 kernels: 16-bit float conversions, the
+// strip-layout constants and the MFMA wrappers.
+//
+// Strip layout (one matrix W[K, N], y = x W, int4 q, group size g | 128):
+//   quant plane: strip s = n / 16, K tile t = k / 128, 1 KiB per (s, t):
+//     byte ((s * kt_pitch + t) * 64 + L) * 16 + 4 * mu holds, for lane L and dword mu in 0..3,
+//     column 16 s + (L & 15) and K = 128 t + 32 mu + 8 (L >> 4) + e, e = 0..7,
+//     nibble p(e) = e / 2 for even e and 4 + e / 2 for odd e.
+//   That is the B-operand order of v_mfma_f32_16x16x32_{f16,bf16}: lane L holds column
+//   L & 15 and 8 consecutive K of one 32-K step. With the nibble order, masking a dword
+//   with 0x000F000F (after a shift by 4 i) gives the pair (e = 2 i, e = 2 i + 1) in the
+//   two 16-bit halves, so OR-ing the exponent of 1024 (fp16) or 128 (bf16) makes the
+//   operand without a conversion instruction.
+//   meta plane: one uint32 record per (strip, group, column):
+//     record ((s * g_pitch + group) * 16 + (n & 15)) = scale bits | zero << 16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hm {
+
+constexpr int kTileK = 128;      // K rows per strip tile
+constexpr int kStrip = 16;       // columns per strip
+constexpr int kTileBytes = 1024; // nibble bytes per strip tile
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round to nearest even; NaN stays NaN (quiet bit set).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return static_cast<uint16_t>((u >> 16) | 0x40u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Activation / scale element type. kMagic is the exponent pattern that turns a nibble in
+// the low mantissa bits into bias + q. kWide is true when the nibble at bits 4..7 of each
+// half also fits the mantissa (fp16: 1024 + 16 q), which saves a shift per pair.
+struct F16 {
+    static constexpr uint32_t kMagic = 0x64006400u;
+    static constexpr float kBias = 1024.0f;
+    static constexpr bool kWide = true;
+    __device__ static __forceinline__ float to_float(uint32_t bits) { return half_bits_to_float(bits); }
+    __device__ static __forceinline__ uint16_t from_float(float f) { return float_to_half_bits(f); }
+    __device__ static __forceinline__ float4_t mfma16(uint4 a, uint4 b, float4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                       0, 0, 0);
+    }
+    __device__ static __forceinline__ float16_t mfma32(uint4 a, uint4 b, float16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                       0, 0, 0);
+    }
+};
+
+struct BF16 {
+    static constexpr uint32_t kMagic = 0x43004300u;
+    static constexpr float kBias = 128.0f;
+    static constexpr bool kWide = false;
+    __device__ static __forceinline__ float to_float(uint32_t bits) { return bf16_bits_to_float(bits); }
+    __device__ static __forceinline__ uint16_t from_float(float f) { return float_to_bf16_bits(f); }
+    __device__ static __forceinline__ float4_t mfma16(uint4 a, uint4 b, float4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                        c, 0, 0, 0);
+    }
+    __device__ static __forceinline__ float16_t mfma32(uint4 a, uint4 b, float16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                        c, 0, 0, 0);
+    }
+};
+
+// Nibble position of K offset e (0..7) inside a strip dword.
+__host__ __device__ __forceinline__ int nibble_of(int e) { return (e & 1) ? 4 + (e >> 1) : (e >> 1); }
+
+// B operand of one 32-K MFMA step from one strip dword: eight values bias + q_e (F16 with
+// kWide: the odd pairs hold bias + 16 q_e, and the caller scales the matching activations by 1/16).
+template <class T> __device__ __forceinline__ uint4 magic_operand(uint32_t w) {
+    uint4 b;
+    if constexpr (T::kWide) {
+        const uint32_t u = w >> 8;
+        b.x = (w & 0x000F000Fu) | T::kMagic;
+        b.y = (w & 0x00F000F0u) | T::kMagic;
+        b.z = (u & 0x000F000Fu) | T::kMagic;
+        b.w = (u & 0x00F000F0u) | T::kMagic;
+    } else {
+        b.x = (w & 0x000F000Fu) | T::kMagic;
+        b.y = ((w >> 4) & 0x000F000Fu) | T::kMagic;
+        b.z = ((w >> 8) & 0x000F000Fu) | T::kMagic;
+        b.w = ((w >> 12) & 0x000F000Fu) | T::kMagic;
+    }
+    return b;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+} // namespace hm

@@ -1,0 +1,89 @@
+// Host-side declarations shared by the C ABI (hm_api.cpp) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace hm {
+
+// Device planes of one repacked matrix (layout: hm_device.hpp).
+struct Planes {
+    const uint8_t *quant = nullptr; // (N/16) * (K/128) KiB
+    const uint32_t *meta = nullptr; // (N/16) * (K/group) * 16 records
+    int64_t K = 0, N = 0, group = 128;
+    int dtype = 0; // hm_dtype
+    int64_t kt_pitch() const { return K / 128; }
+    int64_t g_pitch() const { return K / group; }
+};
+
+// One source matrix of a repack: the reference tiles or logical tensors of a [K, N] matrix.
+struct TileSource {
+    const uint8_t *tiles = nullptr;
+    int64_t tiles_k = 0, tiles_n = 0; // of the whole packed matrix
+};
+struct LogicalSource {
+    const uint8_t *q = nullptr;      // [K, ld] row-major
+    const uint16_t *scales = nullptr; // [K/group, ld]
+    const uint8_t *zeros = nullptr;   // [K/group, ld]
+    int64_t ld = 0;
+};
+
+// Repack launches. `fused` interleaves two sources per 16 columns (strip 2j from src[0], 2j + 1 from src[1]);
+// then N counts the columns of the result (2x the columns taken from each source).
+hipError_t launch_repack_tiles(const TileSource *src, int nsrc, bool fused, uint8_t *quant, uint32_t *meta, int64_t K,
+                               int64_t N, int dtype, hipStream_t stream);
+hipError_t launch_repack_logical(const LogicalSource *src, int nsrc, bool fused, uint8_t *quant, uint32_t *meta,
+                                 int64_t K, int64_t N, int64_t group, hipStream_t stream);
+hipError_t launch_unpack(const Planes &p, uint8_t *q, uint16_t *scales, uint8_t *zeros, hipStream_t stream);
+
+// Decode GEMV (M <= 16) on strips [strip_begin, strip_begin + n/16) and K tiles [kt_begin, kt_begin + kt_count).
+// fused: pairs of strips (gate, up) -> act = SiLU(gate) * up, n = output channels.
+struct GemvCall {
+    Planes w;
+    const uint16_t *x = nullptr;
+    int64_t ldx = 0;
+    uint16_t *y = nullptr;
+    int64_t ldy = 0;
+    int64_t m = 1;
+    int64_t strip_begin = 0;
+    int64_t n = 0; // output columns (plain) or channels (fused)
+    int64_t kt_begin = 0, kt_count = 0;
+    bool fused = false;
+    float *partial = nullptr; // split-K partials, [splits, m, n] fp32
+    int splits = 1;
+    int waves = 4;
+};
+size_t gemv_partial_bytes(const GemvCall &c);
+int gemv_pick_splits(const GemvCall &c);
+size_t gemv_lds_bytes(const GemvCall &c, int splits);
+hipError_t launch_gemv(const GemvCall &c, hipStream_t stream);
+
+// Prefill GEMM (MFMA 32x32x16) with the same operand conventions; fused writes SiLU(gate) * up.
+struct GemmCall {
+    Planes w;
+    const uint16_t *x = nullptr;
+    int64_t ldx = 0;
+    uint16_t *y = nullptr;
+    int64_t ldy = 0;
+    int64_t m = 0;
+    int64_t strip_begin = 0;
+    int64_t n = 0;
+    int64_t kt_begin = 0, kt_count = 0;
+    bool fused = false;
+};
+hipError_t launch_gemm(const GemmCall &c, hipStream_t stream);
+
+hipError_t launch_silu_mul(const uint16_t *gate_up, int64_t ld_in, uint16_t *act, int64_t ld_out, int64_t rows, int64_t n,
+                           bool interleaved, int dtype, hipStream_t stream);
+hipError_t launch_rmsnorm(uint16_t *out, int64_t ld_out, const uint16_t *x, int64_t ldx, const uint16_t *weight,
+                          int64_t rows, int64_t cols, float eps, int dtype, hipStream_t stream);
+hipError_t launch_residual_add2(uint16_t *x, int64_t ldx, const uint16_t *a, int64_t lda, const uint16_t *b, int64_t ldb,
+                                int64_t rows, int64_t cols, int dtype, hipStream_t stream);
+hipError_t launch_residual_rmsnorm(uint16_t *x, int64_t ldx, const uint16_t *y, int64_t ldy, const uint16_t *weight,
+                                   uint16_t *normed, int64_t ld_normed, int64_t rows, int64_t cols, float eps, int dtype,
+                                   hipStream_t stream);
+
+} // namespace hm

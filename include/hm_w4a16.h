@@ -1,0 +1,217 @@
+/*
+ * hm_w4a16.h - C ABI of the MI355X (gfx950) W4A16 SwiGLU FFN engine.
+ *
+ * Plain C: pointers, sizes and status codes only. All tensors are caller-owned
+ * memory; the `stream` arguments are hipStream_t values passed as void*
+ * (NULL means the default stream). Compute entry points enqueue work on that
+ * stream and return without synchronizing; they never allocate.
+ *
+ * Element types: activations, outputs and per-group scales are 16-bit floats,
+ * either bf16 (the reference operator surface) or fp16 (hm_dtype). They are
+ * passed as raw uint16_t bits. Quantized weights are unsigned int4 (0..15)
+ * with unsigned int4 zero points, dequantized as (q - z) * s.
+ *
+ * Errors: every function that can fail returns an hm_status; the message of
+ * the last failure on the calling thread is available from hm_last_error().
+ * This replaces the reference's TORCH_CHECK / std::exit / std::runtime_error
+ * paths (kernels/gpu/src/pack_w4a16.cpp:11-16, unified_llm_w4a16.cpp:889-891,
+ * src/hipkernels/w4a16_gemv_packed.cu:197-200).
+ */
+#ifndef HM_W4A16_H
+#define HM_W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HM_ABI_VERSION 1
+
+typedef enum hm_status {
+    HM_OK = 0,
+    HM_INVALID_ARGUMENT = 1, /* shape, alignment, range or pointer check failed */
+    HM_UNSUPPORTED = 2,      /* valid request that this build does not implement */
+    HM_HIP_ERROR = 3,        /* a HIP runtime call or kernel launch failed */
+    HM_OUT_OF_MEMORY = 4,    /* a create/repack call could not allocate device memory */
+    HM_WORKSPACE_TOO_SMALL = 5
+} hm_status;
+
+typedef enum hm_dtype {
+    HM_BF16 = 0, /* reference surface: include/hipkernels/w4a16_gemm_packed.hpp:31-33 */
+    HM_FP16 = 1
+} hm_dtype;
+
+/* Column order of a reference-packed gate_up matrix
+ * (kernels/gpu/include/heteromega/gpu_ffn.hpp:43-46). */
+typedef enum hm_gate_up_layout {
+    HM_GATE_UP_BLOCKED = 0,    /* [gate 0..n) | up 0..n) ] */
+    HM_GATE_UP_INTERLEAVED = 1 /* per 64 channels: 64 gate columns, then 64 up columns */
+} hm_gate_up_layout;
+
+int hm_abi_version(void);
+const char *hm_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Reference 4352-byte tile format (host memory, no GPU needed).
+ * A [K, N] matrix is (K/128) x (N/64) tiles of 4096 nibble bytes, 64 bf16
+ * scales and 128 zero bytes, in column-group order.
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of a packed [K, N] matrix: (K/128)*(N/64)*4352, or -1 if K%128 or N%64.
+ * Replaces MergedFfnConfig::weight_bytes (include/heteromega/merged_ffn_contract.hpp:60). */
+int64_t hm_packed_bytes(int64_t K, int64_t N);
+
+/* Position of tile (tile column c, tile row r) in a packed matrix of
+ * tiles_k x tiles_n tiles, or -1 when out of range.
+ * Replaces heteromega::packed_tile_index (kernels/gpu/src/pack_w4a16.cpp:100-107). */
+int64_t hm_packed_tile_index(int64_t c, int64_t r, int64_t tiles_k, int64_t tiles_n);
+
+/* Packs q [K, N] (uint8 0..15), scales [K/128, N] (bf16 bits) and zeros
+ * [K/128, N] (int8 0..15), all row-major host arrays, into hm_packed_bytes(K, N)
+ * bytes at `out`. Replaces heteromega::pack_w4a16 (kernels/gpu/src/pack_w4a16.cpp:9-66)
+ * and the packers it mirrors (py/unified_llm_w4a16/llama3_8b_w4a16_model.py:546-656,
+ * src/unified_llm_w4a16_hetero/unified_llm_w4a16.cpp:1242-1387). */
+hm_status hm_pack_w4a16(const uint8_t *q, const uint16_t *scales, const int8_t *zeros, int64_t K, int64_t N,
+                        uint8_t *out);
+
+/* Unpacks AWQ int32 tensors (host): qweight [K, N/8] -> q [K, N] uint8, and
+ * qzeros [G, N/8] -> zeros [G, N] uint8, nibble order 0,4,1,5,2,6,3,7.
+ * Replaces _unpack_awq_qweight / _unpack_awq_qzeros
+ * (py/unified_llm_w4a16/llama3_8b_w4a16_model.py:325-358). */
+hm_status hm_awq_unpack(const int32_t *packed, int64_t rows, int64_t cols8, uint8_t *out);
+
+/* ---------------------------------------------------------------------------
+ * Repacked weights on the device (CDNA4 strip layout). Created once at load
+ * time; the forward entry points read only this layout.
+ * ------------------------------------------------------------------------- */
+typedef struct hm_weights hm_weights;
+
+/* From a reference-packed matrix already in device memory: `tiles` holds the
+ * packed [packed_k, packed_n] matrix (hm_packed_bytes(packed_k, packed_n) bytes).
+ * The repacked matrix is its leading [K, N] block (K%128 == 0, N%16 == 0).
+ * Group size is 128 (the tile height). Replaces the packed_params_ buffer that
+ * QuantizedLinearImpl owns (unified_llm_w4a16.cpp:854) as the kernels' input. */
+hm_status hm_weights_from_tiles(const uint8_t *tiles, int64_t packed_k, int64_t packed_n, int64_t K, int64_t N,
+                                hm_dtype dtype, void *stream, hm_weights **out);
+
+/* From logical device tensors: q [K, N] uint8 (0..15), scales [K/group, N]
+ * (dtype bits), zeros [K/group, N] uint8 (0..15), row-major. group in
+ * {32, 64, 128}. Covers what the 4352-byte layout cannot hold (group 64,
+ * SURVEY finding: packers drop the second group of each tile). */
+hm_status hm_weights_from_logical(const uint8_t *q, const uint16_t *scales, const uint8_t *zeros, int64_t K,
+                                  int64_t N, int64_t group, hm_dtype dtype, void *stream, hm_weights **out);
+
+/* Writes the logical tensors back (device pointers, same shapes as above).
+ * Round trip from_logical -> to_logical is bit-exact. */
+hm_status hm_weights_to_logical(const hm_weights *w, uint8_t *q, uint16_t *scales, uint8_t *zeros, void *stream);
+
+hm_status hm_weights_info(const hm_weights *w, int64_t *K, int64_t *N, int64_t *group, int32_t *dtype,
+                          int64_t *device_bytes);
+
+/* Device pointers of the two planes (nibble tiles, scale/zero records) and their sizes. */
+hm_status hm_weights_planes(const hm_weights *w, const void **quant, int64_t *quant_bytes, const void **meta,
+                            int64_t *meta_bytes);
+
+hm_status hm_weights_destroy(hm_weights *w);
+
+/* ---------------------------------------------------------------------------
+ * One projection: y[M, n] = x[M, k] @ W[:k, :n].
+ * Replaces hipkernels::w4a16_gemv_fused_packed / w4a16_gemm_fused_packed[_tiles]
+ * (include/hipkernels/w4a16_gemm_packed.hpp:38-52) and heteromega::gemv_w4a16,
+ * gemm_w4a16, packed_linear (kernels/gpu/include/heteromega/gpu_ffn.hpp:99-199).
+ * x and y are row-major with leading dimensions ldx, ldy (elements). The
+ * block is the leading k x n of the repacked matrix (k%128 == 0, n%16 == 0).
+ * col_begin selects columns [col_begin, col_begin + n) instead (the
+ * reference GEMV's start_col, w4a16_gemv_packed.cu:178-194); it must be a
+ * multiple of 16. No input padding to 128 rows is needed.
+ * ------------------------------------------------------------------------- */
+size_t hm_linear_workspace_bytes(const hm_weights *w, int64_t M, int64_t k, int64_t n);
+hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t k,
+                    int64_t n, int64_t col_begin, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * One SwiGLU FFN layer: y = (SiLU(x Wg) * (x Wu)) Wd over the channels
+ * [ch_begin, ch_end) of the layer (the row/column partition: the GPU share of
+ * the reference's channel split, kernels/gpu/src/gpu_ffn.cpp:77-119 and
+ * src/unified_llm_w4a16_hetero/merged_ffn.cpp:235-236). Channel bounds are
+ * multiples of 128. SiLU(g)*u is computed in fp32 and rounded once to the
+ * activation dtype (kernels/gpu/src/silu_mul.cu:10-30 semantics).
+ * ------------------------------------------------------------------------- */
+typedef struct hm_ffn hm_ffn;
+
+/* From reference-packed device matrices gate [H, I], up [H, I], down [I, H]
+ * (replaces GpuFfnModel::add_layer, kernels/gpu/src/gpu_ffn.cpp:122-130). */
+hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden,
+                            int64_t inter, hm_dtype dtype, void *stream, hm_ffn **out);
+
+/* From logical device tensors (see hm_weights_from_logical), any group in {32, 64, 128}:
+ * gate/up q [H, I], s/z [H/group, I]; down q [I, H], s/z [I/group, H]. */
+hm_status hm_ffn_from_logical(const uint8_t *gate_q, const uint16_t *gate_s, const uint8_t *gate_z,
+                              const uint8_t *up_q, const uint16_t *up_s, const uint8_t *up_z,
+                              const uint8_t *down_q, const uint16_t *down_s, const uint8_t *down_z, int64_t hidden,
+                              int64_t inter, int64_t group, hm_dtype dtype, void *stream, hm_ffn **out);
+
+hm_status hm_ffn_info(const hm_ffn *f, int64_t *hidden, int64_t *inter, int64_t *group, int32_t *dtype);
+hm_status hm_ffn_destroy(hm_ffn *f);
+
+/* Workspace for hm_ffn_forward with up to max_m rows (the SwiGLU activation
+ * [max_m, I] and split-K partials). Replaces GpuFfnBuffers (gpu_ffn.hpp:172-180). */
+size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m);
+
+/* y [M, H] (ldy) = FFN over channels [ch_begin, ch_end) of x [M, H] (ldx). */
+hm_status hm_ffn_forward(const hm_ffn *f, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M,
+                         int64_t ch_begin, int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The first half alone: act [M, ch_end - ch_begin] (ld_act) = SiLU(x Wg) * (x Wu). */
+hm_status hm_ffn_gate_up(const hm_ffn *f, void *act, int64_t ld_act, const void *x, int64_t ldx, int64_t M,
+                         int64_t ch_begin, int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The second half alone: y [M, H] = act [M, ch_end - ch_begin] @ Wd[ch_begin:ch_end, :]. */
+hm_status hm_ffn_down(const hm_ffn *f, void *y, int64_t ldy, const void *act, int64_t ld_act, int64_t M,
+                      int64_t ch_begin, int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Elementwise operators next to the FFN.
+ * ------------------------------------------------------------------------- */
+
+/* act[m, j] = SiLU(gate[m, j]) * up[m, j], fp32 math, one rounding. gate and up
+ * are columns of gate_up [rows, 2n] in `layout` order. Replaces heteromega::silu_mul
+ * (kernels/gpu/src/silu_mul.cu:34-57). */
+hm_status hm_silu_mul(const void *gate_up, int64_t ld_in, void *act, int64_t ld_out, int64_t rows, int64_t n,
+                      int32_t layout, hm_dtype dtype, void *stream);
+
+/* out = x * rsqrt(mean(x^2) + eps) * weight per row (fp32 math, one rounding).
+ * Replaces launch_rmsnorm (src/hipkernels/rmsnorm.cu:65-103, non-gemma). */
+hm_status hm_rmsnorm(void *out, int64_t ld_out, const void *x, int64_t ldx, const void *weight, int64_t rows,
+                     int64_t cols, float eps, hm_dtype dtype, void *stream);
+
+/* x += a + b per element (a or b may be NULL), fp32 math, one rounding.
+ * Replaces heteromega::residual_add2 (kernels/gpu/src/residual_add.cu:9-73). */
+hm_status hm_residual_add2(void *x, int64_t ldx, const void *a, int64_t lda, const void *b, int64_t ldb,
+                           int64_t rows, int64_t cols, hm_dtype dtype, void *stream);
+
+/* One dispatch between FFN layers: x += y (residual), then normed = RMSNorm(x) * weight.
+ * The layer-boundary fusion of kernels/gpu/src/residual_norm.cu:25-98 without its GEMM input prep. */
+hm_status hm_residual_rmsnorm(void *x, int64_t ldx, const void *y, int64_t ldy, const void *weight, void *normed,
+                              int64_t ld_normed, int64_t rows, int64_t cols, float eps, hm_dtype dtype, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Partition descriptor (host). The other device's share is [0, npu_channels),
+ * the GPU's is [npu_channels, intermediate), as in npu/ffn/reference.py:121-151.
+ * On this build every share runs on the GPU; npu_channels = 0 is the GPU-only case.
+ * ------------------------------------------------------------------------- */
+
+/* Checks 0 <= npu_channels <= intermediate and the alignment (reference.py:127-133). */
+hm_status hm_partition_check(int64_t intermediate, int64_t npu_channels, int64_t alignment);
+
+/* Rounds intermediate * ratio to the nearest multiple of alignment, ties up
+ * (FFNPartition.from_ratio, reference.py:135-144). */
+hm_status hm_partition_from_ratio(int64_t intermediate, double npu_ratio, int64_t alignment, int64_t *npu_channels);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HM_W4A16_H */

@@ -1,0 +1,306 @@
+"""CPU oracle of the W4A16 SwiGLU FFN hot path. TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() (as the checker) and bench.py's cpu_baseline leg use this module.
+The product package heteromega_amd never imports it.
+
+Float math is float64 numpy; byte/bit work and the CPU baseline are in hm_oracle.c (ctypes). Each function
+names the reference code it restates.
+"""
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+_lib = None
+
+TILE_K, TILE_N, TILE_BYTES = 128, 64, 4352
+
+
+def build():
+    """Compiles hm_oracle.c (gcc) into oracle/_build/liboracle.so."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        i64 = ctypes.c_int64
+        L.or_bf16_from_f32.argtypes, L.or_bf16_from_f32.restype = [ctypes.c_float], ctypes.c_uint16
+        L.or_f16_from_f32.argtypes, L.or_f16_from_f32.restype = [ctypes.c_float], ctypes.c_uint16
+        L.or_bf16_round_array.argtypes = [P, P, i64]
+        L.or_f16_round_array.argtypes = [P, P, i64]
+        L.or_tile_index.argtypes, L.or_tile_index.restype = [i64, i64, i64, i64], i64
+        L.or_pack_tiles.argtypes, L.or_pack_tiles.restype = [P, P, P, i64, i64, P], ctypes.c_int
+        L.or_unpack_tiles.argtypes, L.or_unpack_tiles.restype = [P, i64, i64, P, P, P, P], ctypes.c_int
+        L.or_awq_unpack.argtypes = [P, i64, i64, P]
+        L.or_cpu_has_avx512.restype = ctypes.c_int
+        L.or_cpu_gemv_packed.argtypes, L.or_cpu_gemv_packed.restype = [P, P, i64, i64, i64, i64, P, ctypes.c_int, ctypes.c_int], ctypes.c_int
+        L.or_silu_mul_bf16_model.argtypes = [P, P, i64, ctypes.c_int]
+        L.or_cpu_ffn_decode.argtypes, L.or_cpu_ffn_decode.restype = [P, P, P, P, i64, i64, P, P, ctypes.c_int, ctypes.c_int], ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---- 16-bit floats ------------------------------------------------------------------------------------
+
+def bf16_round(values):
+    """Round float32 to bf16, ties to even, keep inf, keep NaN as NaN (npu/ffn/reference.py:26-35).
+    Returns float32 values."""
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(v.shape, np.uint16)
+    lib().or_bf16_round_array(_ptr(v), _ptr(out), v.size)
+    return bf16_bits_to_f32(out)
+
+
+def bf16_bits(values):
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(v.shape, np.uint16)
+    lib().or_bf16_round_array(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def bf16_bits_to_f32(bits):
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_bits(values):
+    """IEEE binary16 round to nearest even (C restatement; pinned against numpy's float16 cast in tests)."""
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(v.shape, np.uint16)
+    lib().or_f16_round_array(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def f16_bits_to_f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def to_bits(values, dtype):
+    """float -> 16-bit pattern of `dtype` ('bf16' or 'fp16')."""
+    return bf16_bits(values) if dtype == "bf16" else f16_bits(values)
+
+
+def from_bits(bits, dtype):
+    return bf16_bits_to_f32(bits) if dtype == "bf16" else f16_bits_to_f32(bits)
+
+
+def round_to(values, dtype):
+    return from_bits(to_bits(values, dtype), dtype)
+
+
+# ---- portable [N, K/2] format of the reference oracle (npu/ffn/reference.py:38-57, :93-98) ---------
+
+def pack_int4(values):
+    """[N, K] unsigned int4 -> [N, K/2] bytes, even K in the low nibble (reference.py:38-46)."""
+    values = np.asarray(values)
+    if values.ndim != 2 or values.shape[1] % 2:
+        raise ValueError("int4 values must have shape [N, even K]")
+    if not np.issubdtype(values.dtype, np.integer) or np.any((values < 0) | (values > 15)):
+        raise ValueError("int4 values must be integers in [0, 15]")
+    v = values.astype(np.uint8)
+    return v[:, 0::2] | (v[:, 1::2] << 4)
+
+
+def unpack_int4(packed):
+    packed = np.asarray(packed, np.uint8)
+    out = np.empty((packed.shape[0], packed.shape[1] * 2), np.uint8)
+    out[:, 0::2] = packed & 15
+    out[:, 1::2] = packed >> 4
+    return out
+
+
+def dequantize_portable(packed, scales, zeros, group):
+    """(q - z) * s of the portable [N, K/2] format, groups along K (reference.py:93-98). float64 [N, K]."""
+    q = unpack_int4(packed).astype(np.float64)
+    s = np.repeat(np.asarray(scales, np.float64), group, axis=1)
+    z = np.repeat(np.asarray(zeros, np.float64), group, axis=1)
+    return (q - z) * s
+
+
+# ---- logical [K, N] weights -------------------------------------------------------------------------
+
+def dequantize(q, scales, zeros, group):
+    """W[K, N] = (q - z) * s, one scale/zero per `group` rows (kernels/gpu/tests/test_gpu_ffn.cpp:75-80). float64."""
+    q = np.asarray(q, np.float64)
+    s = np.repeat(np.asarray(scales, np.float64), group, axis=0)
+    z = np.repeat(np.asarray(zeros, np.float64), group, axis=0)
+    return (q - z) * s
+
+
+def random_weights(rng, k, n, group, dtype, s_lo=0.001, s_hi=0.02, z_lo=0, z_hi=16):
+    """Seeded W4A16 weights with BASELINE's distributions: q uniform 0..15, scales U(s_lo, s_hi) rounded to
+    `dtype` (bits), zeros uniform z_lo..z_hi-1."""
+    q = rng.integers(0, 16, (k, n), dtype=np.uint8)
+    s = to_bits(rng.uniform(s_lo, s_hi, (k // group, n)).astype(np.float32), dtype)
+    z = rng.integers(z_lo, z_hi, (k // group, n), dtype=np.uint8)
+    return q, s, z
+
+
+def weights_f64(q, s_bits, z, group, dtype):
+    return dequantize(q, from_bits(s_bits, dtype), z, group)
+
+
+# ---- 4352-byte tiles ------------------------------------------------------------------------------
+
+def tile_index(c, r, tiles_k, tiles_n):
+    return lib().or_tile_index(c, r, tiles_k, tiles_n)
+
+
+def pack_tiles(q, s_bits, z):
+    """Packer of kernels/gpu/src/pack_w4a16.cpp:9-66 (C restatement). q [K, N] u8, s [K/128, N] bf16 bits,
+    z [K/128, N] u8."""
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(s_bits, np.uint16)
+    z = np.ascontiguousarray(z, np.uint8)
+    k, n = q.shape
+    out = np.empty((k // TILE_K) * (n // TILE_N) * TILE_BYTES, np.uint8)
+    if lib().or_pack_tiles(_ptr(q), _ptr(s), _ptr(z), k, n, _ptr(out)) != 0:
+        raise ValueError("pack_tiles: K must be a multiple of 128 and N of 64")
+    return out
+
+
+def pack_tiles_literal(q, s_bits, z):
+    """numpy restatement of the model's tensor-op packer _pack_weights_packed without padding
+    (py/unified_llm_w4a16/llama3_8b_w4a16_model.py:546-656 and unified_llm_w4a16.cpp:1242-1387): tiles by
+    reshape/permute, zigzag order, nibble pairs of permuted [16, 8, 8, 8] blocks, scales by group index,
+    zeros repeated per 8. An independent route to the same bytes as pack_tiles."""
+    k, n = q.shape
+    scale_flat = np.asarray(s_bits, np.uint16).reshape(-1)
+    zero_flat = np.asarray(z, np.uint8).reshape(-1)
+    group_size = k * n // scale_flat.size
+    ntr, ntc = k // 128, n // 64
+    w_tiles = np.asarray(q, np.uint8).reshape(ntr, 128, ntc, 64).transpose(0, 2, 1, 3).reshape(-1, 128, 64)
+    idx = np.array([r * ntc + c for cm in range(8) for c in range(cm, ntc, 8) for r in range(ntr)])
+    w_perm = w_tiles[idx].reshape(len(idx), 16, 8, 8, 8).transpose(0, 1, 3, 2, 4)
+    packed_w = ((w_perm[..., 0::2] & 0xF) | ((w_perm[..., 1::2] & 0xF) << 4)).astype(np.uint8).reshape(-1, 4096)
+    cols = (idx % ntc)[:, None] * 64 + np.arange(64)
+    group_idx = ((idx // ntc)[:, None] * 128) // group_size
+    sidx = np.clip(group_idx * n + cols, 0, scale_flat.size - 1).ravel()
+    scales_u8 = scale_flat[sidx].reshape(-1, 64).view(np.uint8).reshape(-1, 128)
+    zeros_dup = np.repeat(zero_flat[sidx].reshape(-1, 8, 8), 2, axis=1).reshape(-1, 128)
+    return np.concatenate([packed_w, scales_u8, zeros_dup], 1).ravel()
+
+
+def unpack_tiles(packed, k, n, with_dup=False):
+    """Decoder by the consumer kernels' address formulas (C restatement). Returns q, s_bits, z (and the
+    duplicated zero copy)."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    q = np.empty((k, n), np.uint8)
+    s = np.empty((k // 128, n), np.uint16)
+    z = np.empty((k // 128, n), np.uint8)
+    zd = np.empty((k // 128, n), np.uint8)
+    if lib().or_unpack_tiles(_ptr(packed), k, n, _ptr(q), _ptr(s), _ptr(z), _ptr(zd)) != 0:
+        raise ValueError("unpack_tiles: K must be a multiple of 128 and N of 64")
+    return (q, s, z, zd) if with_dup else (q, s, z)
+
+
+def awq_unpack(packed):
+    """AWQ int32 [rows, cols/8] -> u8 [rows, cols] (llama3_8b_w4a16_model.py:325-358)."""
+    packed = np.ascontiguousarray(packed, np.int32)
+    rows, cols8 = packed.shape
+    out = np.empty((rows, cols8 * 8), np.uint8)
+    lib().or_awq_unpack(_ptr(packed), rows, cols8, _ptr(out))
+    return out
+
+
+# ---- float reference ---------------------------------------------------------------------------------
+
+def silu(v):
+    """SiLU in float64, stable for large |v| (reference.py:163-165)."""
+    v = np.asarray(v, np.float64)
+    e = np.exp(-np.abs(v))
+    return v * np.where(v >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+
+
+def silu_multiply_bf16_io(gate, up):
+    """reference.py:154-171 with bf16_io=True: gate and up rounded, SiLU rounded, product rounded (the
+    model's silu_ then mul_)."""
+    gate = bf16_round(np.asarray(gate, np.float32))
+    up = bf16_round(np.asarray(up, np.float32))
+    s = bf16_round(silu(gate).astype(np.float32))
+    return bf16_round((s.astype(np.float64) * up).astype(np.float32))
+
+
+def ffn(x, gate, up, down, group, dtype, round_act=True, channels=None):
+    """SwiGLU FFN in float64 on exact dtype inputs. gate/up/down are (q, s_bits, z) logical tuples
+    ([H, I] and [I, H]). The activation SiLU(g) * u is rounded to `dtype` once (the single rounding of
+    kernels/gpu/src/silu_mul.cu:10-30), because that rounded value is the down projection's input.
+    channels=(b, e) restricts to a channel slice (reference.py:200-221). Returns (y float64, act)."""
+    x = np.asarray(x, np.float64)
+    wg = weights_f64(*gate, group, dtype)
+    wu = weights_f64(*up, group, dtype)
+    wd = weights_f64(*down, group, dtype)
+    if channels is not None:
+        b, e = channels
+        wg, wu, wd = wg[:, b:e], wu[:, b:e], wd[b:e, :]
+    g = x @ wg
+    u = x @ wu
+    act = silu(g) * u
+    if round_act:
+        act = round_to(act.astype(np.float32), dtype).astype(np.float64)
+    return act @ wd, act
+
+
+def rmsnorm(x, w, eps):
+    """x * rsqrt(mean(x^2) + eps) * w per row (src/hipkernels/rmsnorm.cu:25-62, non-gemma), float64."""
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+
+
+def partition_from_ratio(intermediate, ratio, alignment=128):
+    """FFNPartition.from_ratio: nearest multiple of alignment, ties up (reference.py:135-144)."""
+    if not math.isfinite(ratio) or not 0 <= ratio <= 1:
+        raise ValueError("npu_ratio must be finite and in [0, 1]")
+    return math.floor(intermediate * ratio / alignment + 0.5) * alignment
+
+
+def errors(got, ref):
+    """The reference's metrics (kernels/gpu/tests/test_gpu_ffn.cpp:37-45): max|got-ref| / max|ref|,
+    ||got-ref|| / ||ref||, cosine; plus the raw max abs error."""
+    g = np.asarray(got, np.float64).ravel()
+    r = np.asarray(ref, np.float64).ravel()
+    d = g - r
+    max_rel = np.abs(d).max() / (np.abs(r).max() + 1e-30)
+    rel_l2 = np.linalg.norm(d) / (np.linalg.norm(r) + 1e-30)
+    cos = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r) + 1e-30))
+    return {"max_rel": float(max_rel), "rel_l2": float(rel_l2), "cos": cos, "max_abs": float(np.abs(d).max())}
+
+
+# ---- CPU baseline (restated reference AVX GEMV) ------------------------------------------------------
+
+def cpu_has_avx512():
+    return bool(lib().or_cpu_has_avx512())
+
+
+def cpu_gemv_packed(x_bits, packed, k, n, threads=1, use_avx=-1, start_col=0, end_col=-1):
+    """w4a16_gemv_cpu_fused_packed restated: bf16 x [K] on packed tiles -> bf16 bits [N]."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint16)
+    packed = np.ascontiguousarray(packed, np.uint8)
+    y = np.zeros(n, np.uint16)
+    branch = lib().or_cpu_gemv_packed(_ptr(x_bits), _ptr(packed), k, n, start_col, end_col, _ptr(y), threads, use_avx)
+    return y, branch
+
+
+def cpu_ffn_decode(x_bits, gate_tiles, up_tiles, down_tiles, hidden, inter, threads=1, use_avx=-1, scratch=None, y=None):
+    """The model's CPU decode FFN: gate GEMV, up GEMV, silu_ and mul_ (bf16), down GEMV."""
+    if scratch is None:
+        scratch = np.empty(2 * inter, np.uint16)
+    if y is None:
+        y = np.empty(hidden, np.uint16)
+    branch = lib().or_cpu_ffn_decode(_ptr(x_bits), _ptr(gate_tiles), _ptr(up_tiles), _ptr(down_tiles), hidden, inter, _ptr(scratch),
+                                     _ptr(y), threads, use_avx)
+    return y, branch

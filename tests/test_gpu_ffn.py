@@ -1,0 +1,259 @@
+"""GPU: the SwiGLU FFN layer (fused gate_up + SiLU*up, then down) against the float64 oracle at BASELINE's
+shapes, the channel and row partitions, the GpuFfnModel mirror, and the elementwise operators."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TORCH, assert_close, dev, dev_bits, host_bits, host_f64, logical_to_device, make_x
+
+pytestmark = pytest.mark.gpu
+
+_CACHE = {}
+
+
+def _layer(oracle, hm, device, hidden, inter, group, dtype, seed):
+    """Seeded layer (BASELINE distributions: q, z uniform 0..15, s ~ U(0.001, 0.02)), cached per shape."""
+    key = (hidden, inter, group, dtype, seed)
+    if key not in _CACHE:
+        _CACHE.clear()
+        rng = np.random.default_rng(seed)
+        gate = oracle.random_weights(rng, hidden, inter, group, dtype)
+        up = oracle.random_weights(rng, hidden, inter, group, dtype)
+        down = oracle.random_weights(rng, inter, hidden, group, dtype)
+        layer = hm.FfnLayer.from_logical(logical_to_device(gate, dtype, device), logical_to_device(up, dtype, device),
+                                         logical_to_device(down, dtype, device), group, dtype=TORCH[dtype])
+        wf = tuple(oracle.weights_f64(*w, group, dtype) for w in (gate, up, down))
+        _CACHE[key] = (layer, (gate, up, down), wf)
+    return _CACHE[key]
+
+
+def _ffn_ref(oracle, x64, wf, dtype, channels=None):
+    wg, wu, wd = wf
+    if channels is not None:
+        b, e = channels
+        wg, wu, wd = wg[:, b:e], wu[:, b:e], wd[b:e]
+    act = oracle.silu(x64 @ wg) * (x64 @ wu)
+    act = oracle.round_to(act.astype(np.float32), dtype).astype(np.float64)
+    return act @ wd
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_ffn_decode_llama3_8b(oracle, hm, device, dtype, m):
+    layer, _, wf = _layer(oracle, hm, device, 4096, 14336, 128, dtype, 1)
+    rng = np.random.default_rng(10 + m)
+    x64, x = make_x(oracle, rng, m, 4096, dtype, device)
+    y = layer.forward(x)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, dtype), dtype, f"Llama-3-8B FFN decode M={m}")
+
+
+@pytest.mark.parametrize("dtype,m,rows", [("fp16", 512, None), ("fp16", 2048, 96), ("bf16", 512, 96), ("fp16", 37, None)])
+def test_ffn_prefill_llama3_8b(oracle, hm, device, dtype, m, rows):
+    layer, _, wf = _layer(oracle, hm, device, 4096, 14336, 128, dtype, 1)
+    rng = np.random.default_rng(20 + m)
+    x64, x = make_x(oracle, rng, m, 4096, dtype, device)
+    y = layer.forward(x)
+    torch.cuda.synchronize()
+    sel = np.arange(m) if rows is None else np.sort(rng.choice(m, rows, replace=False))
+    assert_close(oracle, host_f64(y)[sel], _ffn_ref(oracle, x64[sel], wf, dtype), dtype, f"Llama-3-8B FFN prefill M={m}")
+    # rows are independent: a row block alone gives the same bits
+    if m >= 512:
+        y_part = layer.forward(x[128:384].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(y_part, y[128:384])
+
+
+def test_ffn_qwen14b_group64(oracle, hm, device):
+    layer, _, wf = _layer(oracle, hm, device, 5120, 13824, 64, "fp16", 2)
+    rng = np.random.default_rng(30)
+    x64, x = make_x(oracle, rng, 1, 5120, "fp16", device)
+    y = layer.forward(x)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, "fp16"), "fp16", "Qwen2.5-14B FFN g=64 decode")
+    x64, x = make_x(oracle, rng, 1024, 5120, "fp16", device)
+    y = layer.forward(x)
+    torch.cuda.synchronize()
+    sel = np.sort(rng.choice(1024, 64, replace=False))
+    assert_close(oracle, host_f64(y)[sel], _ffn_ref(oracle, x64[sel], wf, "fp16"), "fp16", "Qwen2.5-14B FFN g=64 prefill M=1024")
+
+
+@pytest.mark.parametrize("m", [1, 1024])
+def test_partition_channel_split_qwen(oracle, hm, device, m):
+    # GPU share 75% (10368 channels) and 25% (3456), run one after the other on the GPU,
+    # summed, against the unsplit layer and the oracle.
+    layer, _, wf = _layer(oracle, hm, device, 5120, 13824, 64, "fp16", 2)
+    part = hm.FFNPartition.from_ratio(13824, 0.25)
+    assert part.slices == {"npu": (0, 3456), "gpu": (3456, 13824)}
+    rng = np.random.default_rng(40 + m)
+    x64, x = make_x(oracle, rng, m, 5120, "fp16", device)
+    reduced, partials = hm.ffn_partitioned(layer, x, part)
+    full = layer.forward(x)
+    torch.cuda.synchronize()
+    sel = np.arange(m) if m <= 64 else np.sort(rng.choice(m, 48, replace=False))
+    ref = _ffn_ref(oracle, x64[sel], wf, "fp16")
+    assert_close(oracle, host_f64(reduced)[sel], ref, "fp16", f"channel split 3456/10368 M={m}")
+    assert_close(oracle, host_f64(reduced), host_f64(full), "fp16", f"split vs unsplit M={m}")
+    for dev_name, ch in part.slices.items():
+        assert_close(oracle, host_f64(partials[dev_name])[sel], _ffn_ref(oracle, x64[sel], wf, "fp16", ch), "fp16",
+                     f"share {dev_name} {ch} M={m}")
+    # endpoints: an empty other share is the unsplit layer, bit for bit
+    red0, _ = hm.ffn_partitioned(layer, x, hm.FFNPartition(13824, 0))
+    torch.cuda.synchronize()
+    assert torch.equal(red0, full)
+
+
+def test_partition_row_split_is_exact(oracle, hm, device):
+    layer, _, _ = _layer(oracle, hm, device, 5120, 13824, 64, "fp16", 2)
+    rng = np.random.default_rng(50)
+    _, x = make_x(oracle, rng, 1024, 5120, "fp16", device)
+    full = layer.forward(x)
+    y = torch.empty_like(full)
+    hm.ffn_row_split(layer, x, y, 256)  # GPU rows [0, 768), the other share [768, 1024)
+    torch.cuda.synchronize()
+    assert torch.equal(y, full)
+
+
+@pytest.mark.parametrize("m", [1, 16, 128])
+def test_prefix_equals_separately_packed(oracle, hm, device, m):
+    # Channels [0, s) of the whole layer give the bits of a layer packed from only those channels
+    # (FfnSliceWeights::prefix vs pack_ffn_slice, test_gpu_ffn.cpp:472-481), and [s, I) likewise.
+    rng = np.random.default_rng(60)
+    hidden, inter, s, dtype = 1024, 2048, 768, "bf16"
+    gate = oracle.random_weights(rng, hidden, inter, 128, dtype)
+    up = oracle.random_weights(rng, hidden, inter, 128, dtype)
+    down = oracle.random_weights(rng, inter, hidden, 128, dtype)
+    full = hm.FfnLayer.from_logical(*(logical_to_device(w, dtype, device) for w in (gate, up, down)), 128, dtype=torch.bfloat16)
+    _, x = make_x(oracle, rng, m, hidden, dtype, device)
+    for b, e in ((0, s), (s, inter)):
+        sub = [(w[0][:, b:e].copy(), w[1][:, b:e].copy(), w[2][:, b:e].copy()) for w in (gate, up)]
+        sub.append((down[0][b:e].copy(), down[1][b // 128:e // 128].copy(), down[2][b // 128:e // 128].copy()))
+        part = hm.FfnLayer.from_logical(*(logical_to_device(w, dtype, device) for w in sub), 128, dtype=torch.bfloat16)
+        y_a = full.forward(x, channels=(b, e))
+        y_b = part.forward(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y_a, y_b), (b, e, m)
+
+
+@pytest.mark.parametrize("m", [1, 37, 128])
+def test_gpu_ffn_model_from_reference_tiles(oracle, hm, device, m):
+    # GpuFfnModel from the reference's packed gate/up/down; the GPU owns the prefix [0, s).
+    rng = np.random.default_rng(70)
+    hidden, inter = 1024, 2816
+    gate = oracle.random_weights(rng, hidden, inter, 128, "bf16", 0.002, 0.02, 6, 10)
+    up = oracle.random_weights(rng, hidden, inter, 128, "bf16", 0.002, 0.02, 6, 10)
+    down = oracle.random_weights(rng, inter, hidden, 128, "bf16", 0.002, 0.02, 6, 10)
+    model = hm.GpuFfnModel(torch.bfloat16)
+    model.add_layer(*(dev(oracle.pack_tiles(*w), device) for w in (gate, up, down)), hidden, inter)
+    wf = tuple(oracle.weights_f64(*w, 128, "bf16") for w in (gate, up, down))
+    x64, x = make_x(oracle, rng, m, hidden, "bf16", device, 0.5)
+    y = torch.empty((m, hidden), dtype=torch.bfloat16, device=device)
+    model.forward(0, x, y)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, "bf16"), "bf16", f"GpuFfnModel all channels M={m}")
+    model.set_split(1536, 1024)
+    y_s = torch.empty_like(y)
+    model.forward(0, x, y_s)
+    s = 1536 if m > 1 else 1024
+    y_prefix = model.layer(0).forward(x, channels=(0, s))
+    torch.cuda.synchronize()
+    assert torch.equal(y_s, y_prefix)
+    assert_close(oracle, host_f64(y_s), _ffn_ref(oracle, x64, wf, "bf16", (0, s)), "bf16", f"GpuFfnModel prefix {s} M={m}")
+    with pytest.raises(ValueError):
+        model.set_split(1000, 1024)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_gate_up_and_down_halves(oracle, hm, device, dtype):
+    layer, _, wf = _layer(oracle, hm, device, 4096, 14336, 128, dtype, 1)
+    rng = np.random.default_rng(80)
+    x64, x = make_x(oracle, rng, 4, 4096, dtype, device)
+    act = layer.gate_up(x, channels=(1024, 3072))
+    torch.cuda.synchronize()
+    wg, wu, _ = wf
+    ref_act = oracle.silu(x64 @ wg[:, 1024:3072]) * (x64 @ wu[:, 1024:3072])
+    assert_close(oracle, host_f64(act), ref_act, dtype, "gate_up half")
+    y = layer.down(act, channels=(1024, 3072))
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), host_f64(act) @ wf[2][1024:3072], dtype, "down half")
+
+
+@pytest.mark.parametrize("layout", ["blocked", "interleaved"])
+@pytest.mark.parametrize("m", [1, 37, 2048])
+def test_silu_mul(oracle, hm, device, layout, m):
+    rng = np.random.default_rng(90 + m)
+    n = 7168
+    bits = oracle.bf16_bits((rng.standard_normal((m, 2 * n)) * 4).astype(np.float32))
+    gu = dev_bits(bits, "bf16", device)
+    act = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    hm.silu_mul(gu, act, layout)
+    torch.cuda.synchronize()
+    v = oracle.bf16_bits_to_f32(bits).astype(np.float64)
+    if layout == "blocked":
+        g, u = v[:, :n], v[:, n:]
+    else:
+        pairs = v.reshape(m, n // 64, 2, 64)
+        g, u = pairs[:, :, 0].reshape(m, n), pairs[:, :, 1].reshape(m, n)
+    assert_close(oracle, host_f64(act), oracle.silu(g) * u, "bf16", f"silu_mul {layout} M={m}")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_rmsnorm_and_residuals(oracle, hm, device, dtype):
+    rng = np.random.default_rng(95)
+    m, h = 33, 4096
+    x64, x = make_x(oracle, rng, m, h, dtype, device)
+    a64, a = make_x(oracle, rng, m, h, dtype, device, 0.3)
+    b64, b = make_x(oracle, rng, m, h, dtype, device, 0.3)
+    w64, w = make_x(oracle, rng, 1, h, dtype, device, 0.2)
+    w64 = w64[0] + 1.0
+    w = (w.float() + 1.0).to(TORCH[dtype])
+    w64 = host_f64(w)[0]
+    out = torch.empty_like(x)
+    hm.rmsnorm(out, x, w[0] if w.dim() == 2 else w, 1e-5)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(out), oracle.rmsnorm(x64, w64, 1e-5), dtype, "rmsnorm")
+    xr = x.clone()
+    hm.residual_add2(xr, a, b)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(xr), x64 + (a64 + b64), dtype, "residual_add2")
+    xr2 = x.clone()
+    normed = torch.empty_like(x)
+    hm.residual_rmsnorm(xr2, a, w[0] if w.dim() == 2 else w, normed, 1e-5)
+    torch.cuda.synchronize()
+    xsum = oracle.round_to((x64 + a64).astype(np.float32), dtype).astype(np.float64)
+    assert np.array_equal(host_f64(xr2), xsum)
+    assert_close(oracle, host_f64(normed), oracle.rmsnorm(xsum, w64, 1e-5), dtype, "residual_rmsnorm")
+
+
+def test_ffn_stack_decode_small(oracle, hm, device):
+    # BASELINE config 4 semantics on a small stack: per layer normed = RMSNorm(x); x += FFN(normed).
+    rng = np.random.default_rng(99)
+    hidden, inter, layers, steps, dtype = 512, 1536, 4, 3, "fp16"
+    model = hm.GpuFfnModel(torch.float16)
+    wfs = []
+    for _ in range(layers):
+        ws = [oracle.random_weights(rng, hidden, inter, 128, dtype), oracle.random_weights(rng, hidden, inter, 128, dtype),
+              oracle.random_weights(rng, inter, hidden, 128, dtype)]
+        model.add_layer_logical(*(logical_to_device(w, dtype, device) for w in ws), 128)
+        wfs.append(tuple(oracle.weights_f64(*w, 128, dtype) for w in ws))
+    ones = torch.ones(hidden, dtype=torch.float16, device=device)
+    x64, x = make_x(oracle, rng, 1, hidden, dtype, device)
+    normed = torch.empty_like(x)
+    y = torch.empty_like(x)
+    ref = x64.copy()
+    for _ in range(steps):
+        hm.rmsnorm(normed, x, ones, 1e-5)
+        for i in range(layers):
+            model.forward(i, normed, y)
+            if i + 1 < layers:
+                hm.residual_rmsnorm(x, y, ones, normed, 1e-5)
+            else:
+                hm.residual_add2(x, y)
+            # oracle with the same rounding points: normed, act and y rounded to fp16, x rounded after each add
+            nr = oracle.round_to(oracle.rmsnorm(ref, np.ones(hidden), 1e-5).astype(np.float32), dtype).astype(np.float64)
+            yr = oracle.round_to(_ffn_ref(oracle, nr, wfs[i], dtype).astype(np.float32), dtype).astype(np.float64)
+            ref = oracle.round_to((ref + yr).astype(np.float32), dtype).astype(np.float64)
+        torch.cuda.synchronize()
+        assert_close(oracle, host_f64(x), ref, dtype, "stack step")
+        ref = host_f64(x)  # re-anchor each step so rounding flips do not compound

@@ -1,0 +1,117 @@
+"""GPU: one projection y = x W (decode GEMV for M <= 16, MFMA GEMM above) against the float64 oracle, through
+the C ABI. Covers both dtypes, groups 32/64/128, ragged M, prefixes (leading blocks), start columns and the
+split-K path."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TORCH, assert_close, dev, host_f64, logical_to_device, make_x
+
+pytestmark = pytest.mark.gpu
+
+
+def _matrix(oracle, hm, rng, k, n, group, dtype, device):
+    w_np = oracle.random_weights(rng, k, n, group, dtype)
+    w = hm.RepackedMatrix.from_logical(*logical_to_device(w_np, dtype, device), group, dtype=TORCH[dtype])
+    return w_np, w
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 9, 16, 17, 37, 128, 300])
+def test_linear_vs_oracle(oracle, hm, device, dtype, m):
+    rng = np.random.default_rng(100 + m)
+    k, n, g = 2048, 1024, 128
+    w_np, w = _matrix(oracle, hm, rng, k, n, g, dtype, device)
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=TORCH[dtype], device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    ref = x64 @ oracle.weights_f64(*w_np, g, dtype)
+    assert_close(oracle, host_f64(y), ref, dtype, f"linear M={m} [{k}x{n}] g={g}")
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("m", [1, 4, 16, 64])
+def test_linear_small_groups(oracle, hm, device, group, m):
+    rng = np.random.default_rng(200 + group + m)
+    k, n, dtype = 1024, 512, "fp16"
+    w_np, w = _matrix(oracle, hm, rng, k, n, group, dtype, device)
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=torch.float16, device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, group, dtype), dtype, f"linear g={group} M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 16, 128])
+def test_linear_prefix_and_start_column(oracle, hm, device, m):
+    # leading k x n block of a larger matrix, and columns [col, col + n)
+    rng = np.random.default_rng(300 + m)
+    K, N, dtype = 2048, 1024, "bf16"
+    w_np, w = _matrix(oracle, hm, rng, K, N, 128, dtype, device)
+    wf = oracle.weights_f64(*w_np, 128, dtype)
+    for k, n, col in [(1024, 512, 0), (2048, 256, 512), (512, 128, 896)]:
+        x64, x = make_x(oracle, rng, m, k, dtype, device)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+        hm.packed_linear(y, x, w, k=k, n=n, col_begin=col)
+        torch.cuda.synchronize()
+        assert_close(oracle, host_f64(y), x64 @ wf[:k, col:col + n], dtype, f"prefix k={k} n={n} col={col} M={m}")
+
+
+def test_linear_split_k_path(oracle, hm, device):
+    # M = 16 with K = 14336 does not fit the activation stage in LDS: the GEMV splits K and sums partials.
+    rng = np.random.default_rng(400)
+    k, n, dtype = 14336, 512, "fp16"
+    w_np, w = _matrix(oracle, hm, rng, k, n, 128, dtype, device)
+    assert w.workspace_bytes(16) > 0
+    x64, x = make_x(oracle, rng, 16, k, dtype, device)
+    y = torch.empty((16, n), dtype=torch.float16, device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, 128, dtype), dtype, "split-K M=16 K=14336")
+
+
+def test_linear_strided_rows(oracle, hm, device):
+    # x and y as row views of wider buffers (leading dimensions > width)
+    rng = np.random.default_rng(500)
+    k, n, dtype = 1024, 256, "fp16"
+    w_np, w = _matrix(oracle, hm, rng, k, n, 128, dtype, device)
+    for m in (1, 8, 40):
+        x64, xw = make_x(oracle, rng, m, k + 64, dtype, device)
+        yw = torch.zeros((m, n + 32), dtype=torch.float16, device=device)
+        hm.packed_linear(yw[:, :n], xw[:, :k], w)
+        torch.cuda.synchronize()
+        assert_close(oracle, host_f64(yw[:, :n]), x64[:, :k] @ oracle.weights_f64(*w_np, 128, dtype), dtype, f"strided M={m}")
+        assert torch.all(yw[:, n:] == 0)
+
+
+def test_reference_tiles_decode_path(oracle, hm, device):
+    # The drop-in route: bf16 weights from reference 4352-byte tiles, M = 1 (hipkernels::w4a16_gemv_fused_packed).
+    rng = np.random.default_rng(600)
+    k, n = 4096, 1024
+    w_np = oracle.random_weights(rng, k, n, 128, "bf16", 0.002, 0.02, 6, 10)
+    w = hm.RepackedMatrix.from_tiles(dev(oracle.pack_tiles(*w_np), device), k, n, dtype=torch.bfloat16)
+    x64, x = make_x(oracle, rng, 1, k, "bf16", device, 0.5)
+    y = torch.empty((1, n), dtype=torch.bfloat16, device=device)
+    hm.gemv_w4a16(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, 128, "bf16"), "bf16", "tiles gemv")
+
+
+def test_constant_input_exact(oracle, hm, device):
+    # x = 1/16, q = 9, z = 8, s = 1/16, K = 2048 gives exactly 8 (docs/progress.md:457-460), decode and GEMM.
+    k, n = 2048, 64
+    q = torch.full((k, n), 9, dtype=torch.uint8, device=device)
+    z = torch.full((k // 128, n), 8, dtype=torch.uint8, device=device)
+    for dt in (torch.float16, torch.bfloat16):
+        s = torch.full((k // 128, n), 1 / 16, dtype=dt, device=device)
+        w = hm.RepackedMatrix.from_logical(q, s, z, 128, dtype=dt)
+        for m in (1, 4, 300):
+            x = torch.full((m, k), 1 / 16, dtype=dt, device=device)
+            y = torch.empty((m, n), dtype=dt, device=device) if n % 128 == 0 or m <= 16 else None
+            if y is None:
+                continue
+            hm.packed_linear(y, x, w)
+            torch.cuda.synchronize()
+            assert torch.all(y.float() == 8.0), (dt, m)
