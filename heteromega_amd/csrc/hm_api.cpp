@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -118,11 +119,29 @@ hm_status check_logical(const uint8_t *q, const uint16_t *s, const uint8_t *z, i
 // Rows beyond this use the MFMA GEMM; up to it, the decode GEMV.
 constexpr int64_t kGemvMaxRows = 16;
 
-int gemv_waves(int64_t kt_count, bool fused) {
-    if (fused) {
-        return 4;
+// Waves per decode-GEMV workgroup. HM_GEMV_FUSED_WAVES / HM_GEMV_PLAIN_WAVES override the defaults (tuning).
+int env_int(const char *name, int fallback) {
+    const char *v = std::getenv(name);
+    return v != nullptr && *v != '\0' ? std::atoi(v) : fallback;
+}
+
+// Enough waves that each holds at most one batch of tiles (16, or 8 for group 32), between 4 and 16 waves.
+int gemv_waves(int64_t kt_count, bool fused, int64_t group) {
+    static const int fused_waves = env_int("HM_GEMV_FUSED_WAVES", 0);
+    static const int plain_waves = env_int("HM_GEMV_PLAIN_WAVES", 0);
+    if (fused && fused_waves > 0) {
+        return fused_waves;
     }
-    return kt_count >= 32 ? 8 : 4;
+    if (!fused && plain_waves > 0) {
+        return plain_waves;
+    }
+    const int64_t batch = group >= 64 ? 16 : 8;
+    const int64_t tiles = fused ? 2 * kt_count : kt_count;
+    int waves = 4;
+    while (waves < 16 && tiles > waves * batch) {
+        waves *= 2;
+    }
+    return waves;
 }
 
 hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t strip_begin,
@@ -141,7 +160,7 @@ hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, i
         c.kt_begin = kt_begin;
         c.kt_count = kt_count;
         c.fused = fused;
-        c.waves = gemv_waves(kt_count, fused);
+        c.waves = gemv_waves(kt_count, fused, p.group);
         c.splits = hm::gemv_pick_splits(c);
         const size_t need = hm::gemv_partial_bytes(c);
         if (need > workspace_bytes) {
@@ -182,7 +201,7 @@ size_t linear_workspace(const hm::Planes &p, int64_t M, int64_t n, int64_t kt_co
     c.n = n;
     c.kt_count = kt_count;
     c.fused = fused;
-    c.waves = gemv_waves(kt_count, fused);
+    c.waves = gemv_waves(kt_count, fused, p.group);
     return hm::gemv_partial_bytes(c);
 }
 

@@ -87,24 +87,40 @@ struct BF16 {
 // Nibble position of K offset e (0..7) inside a strip dword.
 __host__ __device__ __forceinline__ int nibble_of(int e) { return (e & 1) ? 4 + (e >> 1) : (e >> 1); }
 
+// Loop-invariant constants of the operand build, held in VGPRs. With all three operands in registers,
+// instruction selection turns (w & mask) | bits into one v_and_or_b32 (gfx9 VOP3 takes no literal). The
+// empty asm only hides the constant values from the optimizer; it runs once per kernel.
+struct MagicRegs {
+    uint32_t lo, hi, magic;
+};
+
+template <class T> __device__ __forceinline__ MagicRegs magic_regs() {
+    MagicRegs r{0x000F000Fu, 0x00F000F0u, T::kMagic};
+    asm volatile("" : "+v"(r.lo), "+v"(r.hi), "+v"(r.magic));
+    return r;
+}
+
 // B operand of one 32-K MFMA step from one strip dword: eight values bias + q_e (F16 with
 // kWide: the odd pairs hold bias + 16 q_e, and the caller scales the matching activations by 1/16).
-template <class T> __device__ __forceinline__ uint4 magic_operand(uint32_t w) {
+template <class T> __device__ __forceinline__ uint4 magic_operand(uint32_t w, const MagicRegs &c) {
     uint4 b;
     if constexpr (T::kWide) {
         const uint32_t u = w >> 8;
-        b.x = (w & 0x000F000Fu) | T::kMagic;
-        b.y = (w & 0x00F000F0u) | T::kMagic;
-        b.z = (u & 0x000F000Fu) | T::kMagic;
-        b.w = (u & 0x00F000F0u) | T::kMagic;
+        b.x = (w & c.lo) | c.magic;
+        b.y = (w & c.hi) | c.magic;
+        b.z = (u & c.lo) | c.magic;
+        b.w = (u & c.hi) | c.magic;
     } else {
-        b.x = (w & 0x000F000Fu) | T::kMagic;
-        b.y = ((w >> 4) & 0x000F000Fu) | T::kMagic;
-        b.z = ((w >> 8) & 0x000F000Fu) | T::kMagic;
-        b.w = ((w >> 12) & 0x000F000Fu) | T::kMagic;
+        b.x = (w & c.lo) | c.magic;
+        b.y = ((w >> 4) & c.lo) | c.magic;
+        b.z = ((w >> 8) & c.lo) | c.magic;
+        b.w = ((w >> 12) & c.lo) | c.magic;
     }
     return b;
 }
+
+// Wave-uniform value as a scalar (lets the compiler keep wave indices and tile loops in SGPRs).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 

@@ -3,7 +3,8 @@
 // Work split. Workgroup = `waves` wave64s over one unit: one strip (16 columns) or, fused, a strip pair
 // (gate and up of the same 16 channels). The unit's K tiles are dealt to its waves round-robin. A wave reads
 // one 1 KiB strip tile per step with one 16-byte load per lane, so each wave load instruction is fully
-// coalesced, and keeps `kBatch` tiles in flight.
+// coalesced. A wave requests its tiles in batches of up to 16 (one memory round trip per batch), after the
+// activation chunks that the workgroup stages in LDS.
 //
 // Math per strip tile (4 MFMA steps of 32 K): the B operand is bias + q straight from the nibbles
 // (hm_device.hpp), A is the activation rows from LDS (rows >= m are zero), so
@@ -24,7 +25,6 @@
 namespace hm {
 namespace {
 
-constexpr int kBatch = 8; // strip tiles in flight per wave
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -43,17 +43,18 @@ struct GemvArgs {
 };
 
 // Dynamic LDS: xs [m][KC] 16-bit, sums [m][KC / G] float2 (Xb, X), red [waves][m][16] float.
-template <class T, int MT, int G, bool FUSED>
-__global__ void __launch_bounds__(512) gemv_kernel(GemvArgs a) {
+template <class T, int MT, int G, bool FUSED, int WGS>
+__global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NS = FUSED ? 2 : 1;
     constexpr int ROWS = MT < 4 ? MT : 4; // D elements per lane that can hold a real row
     constexpr int GPT = 128 / G;          // groups per strip tile
     constexpr int SPG = 4 / GPT;          // MFMA steps per group
+    constexpr int KB = G >= 64 ? 16 : 8;  // weight tiles per wave per batch
 
     const int tid = threadIdx.x;
-    const int waves = blockDim.x >> 6;
-    const int wave = tid >> 6;
+    const int waves = WGS / 64;
+    const int wave = uniform(tid >> 6);
     const int lane = tid & 63;
     const int m = a.m;
 
@@ -68,64 +69,116 @@ __global__ void __launch_bounds__(512) gemv_kernel(GemvArgs a) {
     float2 *sums = reinterpret_cast<float2 *>(smem + ((static_cast<size_t>(m) * kc * 2 + 15) & ~size_t(15)));
     float *red = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(sums) + static_cast<size_t>(m) * kg * sizeof(float2));
 
-    // 1. Stage x (fp16: odd pairs scaled by 1/16) and the per-group sums. Consecutive lanes take consecutive
-    //    8-element chunks of a row, so one group is G / 8 consecutive lanes.
-    {
-        constexpr int CPG = G / 8; // chunks per group
-        const int chunks_row = kc / 8;
-        const int total = m * chunks_row;
-        for (int base = 0; base < total; base += blockDim.x) {
-            const int idx = base + tid;
-            const bool valid = idx < total;
-            float sa = 0.0f, sb = 0.0f;
-            int row = 0, c8 = 0;
-            if (valid) {
-                row = idx / chunks_row;
-                c8 = idx - row * chunks_row;
-                uint4 v = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + c8 * 8);
-                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    const float lo = T::to_float(w[p] & 0xFFFFu), hi = T::to_float(w[p] >> 16);
-                    if (p & 1) {
-                        sb += lo + hi;
-                    } else {
-                        sa += lo + hi;
-                    }
-                }
-                if constexpr (T::kWide) {
-                    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-                    const h2 sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-                    v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
-                    v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
-                }
-                *reinterpret_cast<uint4 *>(xs + row * kc + c8 * 8) = v;
-            }
-#pragma unroll
-            for (int off = 1; off < CPG; off <<= 1) {
-                sa += __shfl_xor(sa, off);
-                sb += __shfl_xor(sb, off);
-            }
-            if (valid && (c8 % CPG) == 0) {
-                const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
-                sums[row * kg + c8 / CPG] = make_float2(xb, sa + sb);
-            }
-        }
-    }
-    __syncthreads();
-
-    // 2. Stream the strip tiles.
+    // Tile stream of this wave: strip `strip`, local tiles wi, wi + wps, ...
     const int wps = waves / NS;          // waves per strip
     const int j = FUSED ? (wave & 1) : 0; // strip of this wave within the unit
     const int wi = FUSED ? (wave >> 1) : wave;
     const int strip = a.strip_begin + blockIdx.x * NS + j;
-    const uint4 *qp = a.quant + (static_cast<int64_t>(strip) * a.kt_pitch + kt0) * 64 + lane;
+    const uint4 *qp = a.quant + (static_cast<int64_t>(strip) * a.kt_pitch + kt0) * 64; // wave-uniform base
     const int col = lane & 15;
     const int h = lane >> 4;
     const uint32_t *mp = a.meta + (static_cast<int64_t>(strip) * a.g_pitch + static_cast<int64_t>(kt0) * GPT) * 16 + col;
-    const int arow = lane & 15; // A-operand row of this lane
-    const bool arow_ok = arow < m;
-    const uint16_t *xa = xs + (arow_ok ? arow : 0) * kc + 8 * h;
+    const int step = wps * KB; // local tiles between two batches of this wave
+
+    // Memory requests go out in this order: the activation chunks this thread stages, then the wave's whole
+    // first batch of weight tiles. Staging waits for the activations only, so one batch costs one round trip.
+    constexpr int CPG = G / 8; // 8-element activation chunks per group
+    const int chunks_row = kc / 8;
+    const int total = m * chunks_row;
+    constexpr int kPre = 4; // chunks per thread held in registers before the weights are requested
+    const bool pre = total <= kPre * WGS;
+    uint4 xv[kPre];
+    if (pre) {
+#pragma unroll
+        for (int c = 0; c < kPre; ++c) {
+            const int idx = c * WGS + tid;
+            if (idx < total) {
+                const int row = idx / chunks_row;
+                xv[c] = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
+            }
+        }
+    }
+
+    uint4 wq[KB];
+    uint32_t rq[KB][GPT];
+    auto load = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int i = i0 + u * wps;
+            if (i < nkt) {
+                const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(qp + i * 64 + lane));
+                wq[u] = uint4{v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int g = 0; g < GPT; ++g) {
+                    rq[u][g] = mp[(i * GPT + g) * 16];
+                }
+            }
+        }
+    };
+    load(wi);
+
+    // 1. Stage x (fp16: odd pairs scaled by 1/16) and the per-group sums. Consecutive lanes take consecutive
+    //    8-element chunks of a row, so one group is G / 8 consecutive lanes.
+    auto stage = [&](int idx, uint4 v, bool valid) {
+        float sa = 0.0f, sb = 0.0f;
+        int row = 0, c8 = 0;
+        if (valid) {
+            row = idx / chunks_row;
+            c8 = idx - row * chunks_row;
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float lo = T::to_float(w[p] & 0xFFFFu), hi = T::to_float(w[p] >> 16);
+                if (p & 1) {
+                    sb += lo + hi;
+                } else {
+                    sa += lo + hi;
+                }
+            }
+            if constexpr (T::kWide) {
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const h2 sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+                v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
+                v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
+            }
+            *reinterpret_cast<uint4 *>(xs + row * kc + c8 * 8) = v;
+        }
+#pragma unroll
+        for (int off = 1; off < CPG; off <<= 1) {
+            sa += __shfl_xor(sa, off);
+            sb += __shfl_xor(sb, off);
+        }
+        if (valid && (c8 % CPG) == 0) {
+            const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
+            sums[row * kg + c8 / CPG] = make_float2(xb, sa + sb);
+        }
+    };
+    if (pre) {
+#pragma unroll
+        for (int c = 0; c < kPre; ++c) {
+            const int idx = c * WGS + tid;
+            stage(idx, xv[c], idx < total); // all lanes take part in the shuffles
+        }
+    } else {
+        for (int base = 0; base < total; base += WGS) {
+            const int idx = base + tid;
+            const bool valid = idx < total;
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (valid) {
+                const int row = idx / chunks_row;
+                v = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
+            }
+            stage(idx, v, valid);
+        }
+    }
+    __syncthreads();
+
+    // 2. Multiply.
+    // A-operand row of this lane. Rows >= m read row m - 1 instead of zeros: they only feed D rows >= m,
+    // which are never stored.
+    const int arow = min(lane & 15, m - 1);
+    const uint16_t *xa = xs + arow * kc + 8 * h;
+    const MagicRegs magic = magic_regs<T>();
 
     float acc[ROWS];
 #pragma unroll
@@ -138,43 +191,26 @@ __global__ void __launch_bounds__(512) gemv_kernel(GemvArgs a) {
         srow[e] = min(4 * h + e, m - 1);
     }
 
-    for (int i0 = wi; i0 < nkt; i0 += wps * kBatch) {
-        uint4 wq[kBatch];
-        uint32_t rec[kBatch][GPT];
+    auto compute = [&](int i0) {
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = i0 + u * wps;
-            if (i < nkt) {
-                const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(qp + static_cast<int64_t>(i) * 64));
-                wq[u] = uint4{v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int g = 0; g < GPT; ++g) {
-                    rec[u][g] = mp[(i * GPT + g) * 16];
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
+        for (int u = 0; u < KB; ++u) {
             const int i = i0 + u * wps;
             if (i < nkt) {
                 const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
                 float4_t p = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int mu = 0; mu < 4; ++mu) {
-                    uint4 av = {0u, 0u, 0u, 0u};
-                    if (arow_ok) {
-                        av = *reinterpret_cast<const uint4 *>(xa + i * 128 + 32 * mu);
-                    }
-                    const uint4 bv = magic_operand<T>(words[mu]);
+                    const uint4 av = *reinterpret_cast<const uint4 *>(xa + i * 128 + 32 * mu);
+                    const uint4 bv = magic_operand<T>(words[mu], magic);
                     if (mu % SPG == 0) {
                         p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
                     }
                     p = T::mfma16(av, bv, p);
                     if (mu % SPG == SPG - 1) {
                         const int g = mu / SPG;
-                        const uint32_t r = rec[u][g];
-                        const float s = T::to_float(r & 0xFFFFu);
-                        const float z = static_cast<float>((r >> 16) & 0xFFu);
+                        const uint32_t rr = rq[u][g];
+                        const float s = T::to_float(rr & 0xFFFFu);
+                        const float z = static_cast<float>((rr >> 16) & 0xFFu);
                         const int gl = i * GPT + g; // local group index
 #pragma unroll
                         for (int e = 0; e < ROWS; ++e) {
@@ -185,6 +221,13 @@ __global__ void __launch_bounds__(512) gemv_kernel(GemvArgs a) {
                     }
                 }
             }
+        }
+    };
+
+    for (int i0 = wi; i0 < nkt; i0 += step) {
+        compute(i0);
+        if (i0 + step < nkt) {
+            load(i0 + step);
         }
     }
 
@@ -197,7 +240,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(GemvArgs a) {
         }
     }
     __syncthreads();
-    for (int o = tid; o < m * 16; o += blockDim.x) {
+    for (int o = tid; o < m * 16; o += WGS) {
         const int row = o >> 4;
         const int c = o & 15;
         float v[NS];
@@ -236,8 +279,9 @@ __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ part
     y[row * ldy + c] = T::from_float(v);
 }
 
-template <class T, int MT, int G, bool FUSED> hipError_t launch_t(const GemvArgs &a, dim3 grid, int threads, size_t lds, hipStream_t s) {
-    auto kern = gemv_kernel<T, MT, G, FUSED>;
+template <class T, int MT, int G, bool FUSED, int WGS>
+hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
+    auto kern = gemv_kernel<T, MT, G, FUSED, WGS>;
     static bool configured = false; // one attribute call per instantiation
     if (!configured) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -246,12 +290,21 @@ template <class T, int MT, int G, bool FUSED> hipError_t launch_t(const GemvArgs
         }
         configured = true;
     }
-    hipLaunchKernelGGL(kern, grid, dim3(threads), lds, s, a);
+    hipLaunchKernelGGL(kern, grid, dim3(WGS), lds, s, a);
     return hipGetLastError();
 }
 
+// Fused (gate/up pairs) runs 4 or 8 waves per workgroup, plain 4, 8 or 16.
 template <class T, int MT, int G> hipError_t launch_g(const GemvArgs &a, bool fused, dim3 grid, int threads, size_t lds, hipStream_t s) {
-    return fused ? launch_t<T, MT, G, true>(a, grid, threads, lds, s) : launch_t<T, MT, G, false>(a, grid, threads, lds, s);
+    if (fused) {
+        return threads >= 512 ? launch_w<T, MT, G, true, 512>(a, grid, lds, s) : launch_w<T, MT, G, true, 256>(a, grid, lds, s);
+    }
+    if constexpr (G == 128 && MT == 1) { // other shapes need more registers than 16 waves per CU allow
+        if (threads >= 1024) {
+            return launch_w<T, MT, G, false, 1024>(a, grid, lds, s);
+        }
+    }
+    return threads >= 512 ? launch_w<T, MT, G, false, 512>(a, grid, lds, s) : launch_w<T, MT, G, false, 256>(a, grid, lds, s);
 }
 
 template <class T, int MT> hipError_t launch_m(const GemvArgs &a, int group, bool fused, dim3 grid, int threads, size_t lds, hipStream_t s) {
@@ -280,12 +333,20 @@ constexpr size_t kLdsBudget = 96 * 1024;
 } // namespace
 
 namespace {
+// Waves per workgroup that a launch uses for c.waves.
+int effective_waves(const GemvCall &c) {
+    if (c.fused) {
+        return c.waves >= 8 ? 8 : 4;
+    }
+    return (c.waves >= 16 && c.w.group == 128 && c.m == 1) ? 16 : c.waves >= 8 ? 8 : 4;
+}
+
 // LDS of one workgroup that stages kt_per_split K tiles.
 size_t lds_for(const GemvCall &c, int64_t kt_per_split) {
     const int64_t kc = kt_per_split * 128;
     const size_t xs = (static_cast<size_t>(c.m) * kc * 2 + 15) & ~size_t(15);
     const size_t sums = static_cast<size_t>(c.m) * (kc / c.w.group) * sizeof(float2);
-    const size_t red = static_cast<size_t>(c.waves) * c.m * 16 * sizeof(float);
+    const size_t red = static_cast<size_t>(effective_waves(c)) * c.m * 16 * sizeof(float);
     return xs + sums + red;
 }
 } // namespace
@@ -329,7 +390,7 @@ hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
     a.partial = real_splits > 1 ? c.partial : nullptr;
     const int units = static_cast<int>(c.n / 16);
     const dim3 grid(units, real_splits);
-    const int threads = c.waves * 64;
+    const int threads = effective_waves(c) * 64;
     const size_t lds = lds_for(c, a.kt_per_split);
     const int group = static_cast<int>(c.w.group);
     hipError_t e = c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, grid, threads, lds, stream)
