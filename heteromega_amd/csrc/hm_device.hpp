@@ -11,8 +11,10 @@
 //   with 0x000F000F (after a shift by 4 i) gives the pair (e = 2 i, e = 2 i + 1) in the
 //   two 16-bit halves, so OR-ing the exponent of 1024 (fp16) or 128 (bf16) makes the
 //   operand without a conversion instruction.
-//   meta plane: one uint32 record per (strip, group, column):
-//     record ((s * g_pitch + group) * 16 + (n & 15)) = scale bits | zero << 16.
+//   meta plane: one uint32 record per (strip, column, group), blocked like the quant plane: the records of
+//   tile (s, t) are 16 columns x (128 / g) groups, contiguous, groups innermost, so a lane's records for a
+//   tile are one 4-, 8- or 16-byte load and a wave's records for a tile share one cache line or two:
+//     record ((s * kt_pitch + t) * 16 + (n & 15)) * (128 / g) + (k % 128) / g = scale bits | zero << 16.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -117,6 +119,17 @@ template <class T> __device__ __forceinline__ uint4 magic_operand(uint32_t w, co
         b.w = ((w >> 12) & c.lo) | c.magic;
     }
     return b;
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations and is a compiler memory
+// barrier, but unlike __syncthreads() it does not wait for the wave's outstanding global loads (the
+// workgroup-scope fence of __syncthreads() waits for vmcnt(0)).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt and lgkmcnt left at "no wait").
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
 // Wave-uniform value as a scalar (lets the compiler keep wave indices and tile loops in SGPRs).

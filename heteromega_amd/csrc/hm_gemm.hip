@@ -27,7 +27,7 @@ struct GemmArgs {
     const uint16_t *x;
     uint16_t *y;
     int64_t ldx, ldy;
-    int kt_pitch, g_pitch;
+    int kt_pitch;
     int kt_begin, kt_count;
     int strip_begin;
     int m;
@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
         for (int c = tid; c < NSTRIP * GPT * 16; c += 256) {
             const int sj = c / (GPT * 16);
             const int r = c % (GPT * 16);
-            ms[c] = a.meta[(static_cast<int64_t>(strip0 + sj) * a.g_pitch + static_cast<int64_t>(t) * GPT) * 16 + r];
+            ms[c] = a.meta[((static_cast<int64_t>(strip0 + sj) * a.kt_pitch + t) * 16 + (r & 15)) * GPT + r / 16];
         }
         __syncthreads();
 
@@ -218,7 +218,6 @@ hipError_t launch_gemm(const GemmCall &c, hipStream_t stream) {
     a.ldx = c.ldx;
     a.ldy = c.ldy;
     a.kt_pitch = static_cast<int>(c.w.kt_pitch());
-    a.g_pitch = static_cast<int>(c.w.g_pitch());
     a.kt_begin = static_cast<int>(c.kt_begin);
     a.kt_count = static_cast<int>(c.kt_count);
     a.strip_begin = static_cast<int>(c.strip_begin);

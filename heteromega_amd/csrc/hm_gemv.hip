@@ -35,7 +35,7 @@ struct GemvArgs {
     uint16_t *y;
     float *partial;
     int64_t ldx, ldy;
-    int kt_pitch, g_pitch;
+    int kt_pitch;
     int kt_begin, kt_count, kt_per_split;
     int strip_begin;
     int m;
@@ -65,11 +65,15 @@ __global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
     const int kg = kc / G;          // groups of this split
     const int64_t xk0 = static_cast<int64_t>(kt0 - a.kt_begin) * 128;
 
+    // Row strides padded by 16 bytes (x) and 8 bytes (sums) so that lanes reading different rows of one MFMA
+    // operand or fold hit different LDS banks.
+    const int xst = kc + 8;  // staged row stride, 16-bit elements
+    const int sst = kg + 1;  // sums row stride, float2
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
-    float2 *sums = reinterpret_cast<float2 *>(smem + ((static_cast<size_t>(m) * kc * 2 + 15) & ~size_t(15)));
-    float *red = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(sums) + static_cast<size_t>(m) * kg * sizeof(float2));
+    float2 *sums = reinterpret_cast<float2 *>(smem + static_cast<size_t>(m) * xst * 2);
+    float *red = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(sums) + static_cast<size_t>(m) * sst * sizeof(float2));
 
-    // Tile stream of this wave: strip `strip`, local tiles wi, wi + wps, ...
+    // Tile stream of this wave: strip `strip`, a contiguous run of its local tiles.
     const int wps = waves / NS;          // waves per strip
     const int j = FUSED ? (wave & 1) : 0; // strip of this wave within the unit
     const int wi = FUSED ? (wave >> 1) : wave;
@@ -77,48 +81,68 @@ __global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
     const uint4 *qp = a.quant + (static_cast<int64_t>(strip) * a.kt_pitch + kt0) * 64; // wave-uniform base
     const int col = lane & 15;
     const int h = lane >> 4;
-    const uint32_t *mp = a.meta + (static_cast<int64_t>(strip) * a.g_pitch + static_cast<int64_t>(kt0) * GPT) * 16 + col;
-    const int step = wps * KB; // local tiles between two batches of this wave
+    const uint32_t *mp = a.meta + ((static_cast<int64_t>(strip) * a.kt_pitch + kt0) * 16 + col) * GPT;
+    // Each wave of a strip takes a contiguous run of tiles [tb, te).
+    const int tpw = (nkt + wps - 1) / wps;
+    const int tb = wi * tpw;
+    const int te = min(tb + tpw, nkt);
 
-    // Memory requests go out in this order: the activation chunks this thread stages, then the wave's whole
-    // first batch of weight tiles. Staging waits for the activations only, so one batch costs one round trip.
-    constexpr int CPG = G / 8; // 8-element activation chunks per group
+    // Memory requests go out in this order: the activation chunks this thread stages (up to kPre, held in
+    // registers), then the wave's whole first batch of weight tiles and records. Staging then waits for the
+    // activations only, so it costs one round trip and never waits for the weights. (LDS DMA loads would
+    // save the registers, but the compiler then waits for vmcnt(0) before every LDS read.)
+    constexpr int CPG = G / 8;              // 8-element activation chunks per group
+    constexpr int kPre = MT == 1 ? 4 : 8;   // chunks per thread staged ahead of the weights
     const int chunks_row = kc / 8;
     const int total = m * chunks_row;
-    constexpr int kPre = 4; // chunks per thread held in registers before the weights are requested
-    const bool pre = total <= kPre * WGS;
     uint4 xv[kPre];
-    if (pre) {
+    auto fetch = [&](int base) { // branch-free: chunks past the end re-read the last one and are not staged
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            const int idx = c * WGS + tid;
-            if (idx < total) {
-                const int row = idx / chunks_row;
-                xv[c] = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
-            }
+            const int idx = min(base + c * WGS + tid, total - 1);
+            const int row = idx / chunks_row;
+            xv[c] = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
         }
-    }
+    };
+    fetch(0);
 
+    // A batch is KB consecutive tiles from i0. Indices past the wave's run are clamped to its last tile, so
+    // the batch has no branches and the compiler can wait for each tile's loads separately (s_waitcnt vmcnt
+    // counting down) instead of for all of them; the clamped copies are weighted by zero.
     uint4 wq[KB];
     uint32_t rq[KB][GPT];
+    // The small record loads go first: folds then wait for them without waiting for the weight tiles.
     auto load = [&](int i0) {
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
-            const int i = i0 + u * wps;
-            if (i < nkt) {
-                const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(qp + i * 64 + lane));
-                wq[u] = uint4{v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int g = 0; g < GPT; ++g) {
-                    rq[u][g] = mp[(i * GPT + g) * 16];
-                }
+            const int i = max(min(i0 + u, te - 1), 0); // a wave without tiles loads tile te - 1 >= 0 and skips it
+            if constexpr (GPT == 1) {
+                rq[u][0] = mp[i * 16];
+            } else if constexpr (GPT == 2) {
+                const uint2 r = *reinterpret_cast<const uint2 *>(mp + i * 32);
+                rq[u][0] = r.x;
+                rq[u][1] = r.y;
+            } else {
+                const uint4 r = *reinterpret_cast<const uint4 *>(mp + i * 64);
+                rq[u][0] = r.x;
+                rq[u][1] = r.y;
+                rq[u][2] = r.z;
+                rq[u][3] = r.w;
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int i = max(min(i0 + u, te - 1), 0);
+            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(qp + i * 64 + lane));
+            wq[u] = uint4{v.x, v.y, v.z, v.w};
+        }
+        __builtin_amdgcn_sched_barrier(0);
     };
-    load(wi);
+    load(tb);
 
-    // 1. Stage x (fp16: odd pairs scaled by 1/16) and the per-group sums. Consecutive lanes take consecutive
-    //    8-element chunks of a row, so one group is G / 8 consecutive lanes.
+    // 1. Stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes take
+    //    consecutive 8-element chunks of a row, so one group is G / 8 consecutive lanes.
     auto stage = [&](int idx, uint4 v, bool valid) {
         float sa = 0.0f, sb = 0.0f;
         int row = 0, c8 = 0;
@@ -141,7 +165,7 @@ __global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
                 v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
                 v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
             }
-            *reinterpret_cast<uint4 *>(xs + row * kc + c8 * 8) = v;
+            *reinterpret_cast<uint4 *>(xs + row * xst + c8 * 8) = v;
         }
 #pragma unroll
         for (int off = 1; off < CPG; off <<= 1) {
@@ -150,34 +174,29 @@ __global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
         }
         if (valid && (c8 % CPG) == 0) {
             const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
-            sums[row * kg + c8 / CPG] = make_float2(xb, sa + sb);
+            sums[row * sst + c8 / CPG] = make_float2(xb, sa + sb);
         }
     };
-    if (pre) {
+#pragma unroll
+    for (int c = 0; c < kPre; ++c) {
+        const int idx = c * WGS + tid;
+        stage(idx, xv[c], idx < total); // all lanes take part in the shuffles
+    }
+    for (int base = kPre * WGS; base < total; base += kPre * WGS) {
+        fetch(base); // large M only: these chunks wait behind the weight batch
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            const int idx = c * WGS + tid;
-            stage(idx, xv[c], idx < total); // all lanes take part in the shuffles
-        }
-    } else {
-        for (int base = 0; base < total; base += WGS) {
-            const int idx = base + tid;
-            const bool valid = idx < total;
-            uint4 v = {0u, 0u, 0u, 0u};
-            if (valid) {
-                const int row = idx / chunks_row;
-                v = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
-            }
-            stage(idx, v, valid);
+            const int idx = base + c * WGS + tid;
+            stage(idx, xv[c], idx < total);
         }
     }
-    __syncthreads();
+    lds_barrier(); // not __syncthreads(): its fence would wait for the weight batch too
 
     // 2. Multiply.
     // A-operand row of this lane. Rows >= m read row m - 1 instead of zeros: they only feed D rows >= m,
     // which are never stored.
     const int arow = min(lane & 15, m - 1);
-    const uint16_t *xa = xs + arow * kc + 8 * h;
+    const uint16_t *xa = xs + arow * xst + 8 * h;
     const MagicRegs magic = magic_regs<T>();
 
     float acc[ROWS];
@@ -194,40 +213,39 @@ __global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
     auto compute = [&](int i0) {
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
-            const int i = i0 + u * wps;
-            if (i < nkt) {
-                const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
-                float4_t p = {0.0f, 0.0f, 0.0f, 0.0f};
+            const int i = min(i0 + u, te - 1);
+            const float live = (i0 + u < te) ? 1.0f : 0.0f;
+            const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
+            float4_t p = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int mu = 0; mu < 4; ++mu) {
-                    const uint4 av = *reinterpret_cast<const uint4 *>(xa + i * 128 + 32 * mu);
-                    const uint4 bv = magic_operand<T>(words[mu], magic);
-                    if (mu % SPG == 0) {
-                        p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
-                    p = T::mfma16(av, bv, p);
-                    if (mu % SPG == SPG - 1) {
-                        const int g = mu / SPG;
-                        const uint32_t rr = rq[u][g];
-                        const float s = T::to_float(rr & 0xFFFFu);
-                        const float z = static_cast<float>((rr >> 16) & 0xFFu);
-                        const int gl = i * GPT + g; // local group index
+            for (int mu = 0; mu < 4; ++mu) {
+                const uint4 av = *reinterpret_cast<const uint4 *>(xa + i * 128 + 32 * mu);
+                const uint4 bv = magic_operand<T>(words[mu], magic);
+                if (mu % SPG == 0) {
+                    p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+                p = T::mfma16(av, bv, p);
+                if (mu % SPG == SPG - 1) {
+                    const int g = mu / SPG;
+                    const uint32_t rr = rq[u][g];
+                    const float s = T::to_float(rr & 0xFFFFu) * live;
+                    const float z = static_cast<float>((rr >> 16) & 0xFFu);
+                    const int gl = i * GPT + g; // local group index
 #pragma unroll
-                        for (int e = 0; e < ROWS; ++e) {
-                            const float2 xsum = sums[srow[e] * kg + gl];
-                            const float t = __builtin_fmaf(-z, xsum.y, p[e] - xsum.x);
-                            acc[e] = __builtin_fmaf(s, t, acc[e]);
-                        }
+                    for (int e = 0; e < ROWS; ++e) {
+                        const float2 xsum = sums[srow[e] * sst + gl];
+                        const float t = __builtin_fmaf(-z, xsum.y, p[e] - xsum.x);
+                        acc[e] = __builtin_fmaf(s, t, acc[e]);
                     }
                 }
             }
         }
     };
 
-    for (int i0 = wi; i0 < nkt; i0 += step) {
+    for (int i0 = tb; i0 < te; i0 += KB) {
         compute(i0);
-        if (i0 + step < nkt) {
-            load(i0 + step);
+        if (i0 + KB < te) {
+            load(i0 + KB);
         }
     }
 
@@ -344,8 +362,8 @@ int effective_waves(const GemvCall &c) {
 // LDS of one workgroup that stages kt_per_split K tiles.
 size_t lds_for(const GemvCall &c, int64_t kt_per_split) {
     const int64_t kc = kt_per_split * 128;
-    const size_t xs = (static_cast<size_t>(c.m) * kc * 2 + 15) & ~size_t(15);
-    const size_t sums = static_cast<size_t>(c.m) * (kc / c.w.group) * sizeof(float2);
+    const size_t xs = static_cast<size_t>(c.m) * (kc + 8) * 2;
+    const size_t sums = static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
     const size_t red = static_cast<size_t>(effective_waves(c)) * c.m * 16 * sizeof(float);
     return xs + sums + red;
 }
@@ -378,7 +396,6 @@ hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
     a.ldx = c.ldx;
     a.ldy = c.ldy;
     a.kt_pitch = static_cast<int>(c.w.kt_pitch());
-    a.g_pitch = static_cast<int>(c.w.g_pitch());
     a.kt_begin = static_cast<int>(c.kt_begin);
     a.kt_count = static_cast<int>(c.kt_count);
     a.strip_begin = static_cast<int>(c.strip_begin);

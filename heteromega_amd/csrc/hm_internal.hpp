@@ -16,7 +16,6 @@ struct Planes {
     int64_t K = 0, N = 0, group = 128;
     int dtype = 0; // hm_dtype
     int64_t kt_pitch() const { return K / 128; }
-    int64_t g_pitch() const { return K / group; }
 };
 
 // One source matrix of a repack: the reference tiles or logical tensors of a [K, N] matrix.

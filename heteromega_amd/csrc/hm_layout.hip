@@ -75,10 +75,9 @@ __global__ void __launch_bounds__(256)
     if (idx >= total) {
         return;
     }
-    const int col = static_cast<int>(idx & 15);
-    const int64_t sg = idx >> 4;
-    const int64_t t = sg % kt; // group == tile row (group size 128)
-    const int64_t s = sg / kt;
+    const int col = static_cast<int>(idx & 15); // group size 128: one record per column and tile
+    const int64_t t = (idx >> 4) % kt;
+    const int64_t s = (idx >> 4) / kt;
     int which;
     int64_t n_src;
     source_column(s * 16 + col, fused, which, n_src);
@@ -116,15 +115,16 @@ __global__ void __launch_bounds__(256)
 }
 
 __global__ void __launch_bounds__(256)
-    repack_logical_meta(LogicalSource s0, LogicalSource s1, bool fused, uint32_t *__restrict__ meta, int64_t groups, int64_t total) {
+    repack_logical_meta(LogicalSource s0, LogicalSource s1, bool fused, uint32_t *__restrict__ meta, int64_t kt, int gpt, int64_t total) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= total) {
         return;
     }
-    const int col = static_cast<int>(idx & 15);
-    const int64_t sg = idx >> 4;
-    const int64_t g = sg % groups;
-    const int64_t s = sg / groups;
+    const int gi = static_cast<int>(idx % gpt);
+    const int col = static_cast<int>((idx / gpt) & 15);
+    const int64_t st = idx / (gpt * 16);
+    const int64_t g = (st % kt) * gpt + gi;
+    const int64_t s = st / kt;
     int which;
     int64_t n_src;
     source_column(s * 16 + col, fused, which, n_src);
@@ -155,15 +155,16 @@ __global__ void __launch_bounds__(256)
 }
 
 __global__ void __launch_bounds__(256) unpack_meta(const uint32_t *__restrict__ meta, uint16_t *__restrict__ scales,
-                                                   uint8_t *__restrict__ zeros, int64_t N, int64_t groups, int64_t total) {
+                                                   uint8_t *__restrict__ zeros, int64_t N, int64_t kt, int gpt, int64_t total) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= total) {
         return;
     }
-    const int col = static_cast<int>(idx & 15);
-    const int64_t sg = idx >> 4;
-    const int64_t g = sg % groups;
-    const int64_t s = sg / groups;
+    const int gi = static_cast<int>(idx % gpt);
+    const int col = static_cast<int>((idx / gpt) & 15);
+    const int64_t st = idx / (gpt * 16);
+    const int64_t g = (st % kt) * gpt + gi;
+    const int64_t s = st / kt;
     const uint32_t rec = meta[idx];
     scales[g * N + s * 16 + col] = static_cast<uint16_t>(rec & 0xFFFFu);
     zeros[g * N + s * 16 + col] = static_cast<uint8_t>(rec >> 16);
@@ -203,7 +204,8 @@ hipError_t launch_repack_logical(const LogicalSource *src, int nsrc, bool fused,
     const int64_t groups = K / group;
     const int64_t records = (N / 16) * groups * 16;
     if (records > 0) {
-        hipLaunchKernelGGL(repack_logical_meta, blocks_for(records), dim3(256), 0, stream, s0, s1, fused, meta, groups, records);
+        hipLaunchKernelGGL(repack_logical_meta, blocks_for(records), dim3(256), 0, stream, s0, s1, fused, meta, kt,
+                           static_cast<int>(128 / group), records);
     }
     return hipGetLastError();
 }
@@ -218,7 +220,8 @@ hipError_t launch_unpack(const Planes &p, uint8_t *q, uint16_t *scales, uint8_t 
     const int64_t groups = p.K / p.group;
     const int64_t records = (p.N / 16) * groups * 16;
     if (records > 0) {
-        hipLaunchKernelGGL(unpack_meta, blocks_for(records), dim3(256), 0, stream, p.meta, scales, zeros, p.N, groups, records);
+        hipLaunchKernelGGL(unpack_meta, blocks_for(records), dim3(256), 0, stream, p.meta, scales, zeros, p.N, kt,
+                           static_cast<int>(128 / p.group), records);
     }
     return hipGetLastError();
 }

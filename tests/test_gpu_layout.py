@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 def decode_strips(quant, meta, k, n, group):
     """numpy reading of the strip layout: tile (s, t) at ((s * K/128 + t) * 64 + L) * 16, dword mu holds column
     16 s + (L & 15), K = 128 t + 32 mu + 8 (L >> 4) + e at nibble e/2 (even e) or 4 + e/2 (odd e); record
-    ((s * K/g + group) * 16 + col) = scale | zero << 16."""
+    ((s * K/128 + t) * 16 + col) * (128/g) + group in tile = scale | zero << 16."""
     words = quant.view(np.uint32).reshape(n // 16, k // 128, 64, 4)
     q = np.empty((k, n), np.uint8)
     nib = np.array([0, 4, 1, 5, 2, 6, 3, 7])
@@ -24,9 +24,11 @@ def decode_strips(quant, meta, k, n, group):
         rows = 128 * t_i + 32 * mu_i + 8 * (l_i >> 4) + e
         cols = 16 * s_i + (l_i & 15)
         q[rows.ravel(), cols.ravel()] = vals.ravel()
-    rec = meta.view(np.uint32).reshape(n // 16, k // group, 16)
-    scales = (rec & 0xFFFF).astype(np.uint16).transpose(1, 0, 2).reshape(k // group, n)
-    zeros = (rec >> 16).astype(np.uint8).transpose(1, 0, 2).reshape(k // group, n)
+    gpt = 128 // group
+    rec = meta.view(np.uint32).reshape(n // 16, k // 128, 16, gpt)  # [strip][tile][column][group in tile]
+    rec = rec.transpose(1, 3, 0, 2).reshape(k // group, n)
+    scales = (rec & 0xFFFF).astype(np.uint16)
+    zeros = (rec >> 16).astype(np.uint8)
     return q, scales, zeros
 
 
