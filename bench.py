@@ -104,19 +104,38 @@ def event_time_graph(torch, g, replays):
 
 
 def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0):
+    """Seconds per decode step (one FFN layer pass): exactly `steps` steps timed, `warmup` untimed before.
+
+    The steps cycle through the weight sets; one graph replay runs one step per set, and a second graph holds
+    the remainder when `steps` is not a multiple of the set count."""
     x = torch.randn((m, h), device=dev).to(layers[0].dtype)
     y = torch.empty_like(x)
     ws = layers[0].workspace(m)
     sets = len(layers)
 
-    def run():
-        for L in layers:
-            L.forward(x, y, workspace=ws)
+    def run(count):
+        def fn():
+            for L in layers[:count]:
+                L.forward(x, y, workspace=ws)
+        return fn
 
-    g = graph_of(torch, run)
-    replays = max(1, steps // sets)
-    sec = time_graph(torch, g, replays, warm_seconds, max(1, warmup // sets))
-    return sec / sets, g, (x, y, ws)
+    g = graph_of(torch, run(sets))
+    rest = steps % sets
+    g_rest = graph_of(torch, run(rest)) if rest else None
+    for _ in range(max(0, warmup) // sets + 1):
+        g.replay()
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + warm_seconds
+    while time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps // sets):
+        g.replay()
+    if g_rest is not None:
+        g_rest.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, g, (x, y, ws)
 
 
 def prefill_bench(hm, torch, dev, layers, m, h, steps, warmup):
@@ -133,6 +152,48 @@ def prefill_bench(hm, torch, dev, layers, m, h, steps, warmup):
     sec = time_graph(torch, g, max(1, steps // 2), 0.0, max(1, warmup // 2))
     del L0
     return sec / 2
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_gemv_gate_up_llama8b_decode_m1.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the fused gate_up GEMV (Llama-3-8B, M = 1), from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy kernel there), or None without one."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def pmc_probe(hm, torch, dev, H, I, G, sets):
+    """Eager launches for one rocprofv3 --pmc pass: a copy kernel of known size (calibration), then the fused
+    gate_up GEMV and the down GEMV of the headline workload, on rotating weight sets."""
+    words = (64 << 20) // 4
+    bufs = [torch.empty(words, dtype=torch.int32, device=dev).random_(0, 1 << 30) for _ in range(4)]
+    outs = [torch.empty_like(b) for b in bufs]
+    torch.cuda.synchronize()
+    for r in range(8):
+        torch.bitwise_not(bufs[r % 4], out=outs[r % 4])
+    torch.cuda.synchronize()
+    log(f"pmc probe: 8 copy launches of {words * 4} bytes read + {words * 4} bytes written")
+    del bufs, outs
+    layers = make_layers(hm, torch, dev, H, I, G, sets)
+    x = torch.randn((1, H), device=dev).to(torch.float16)
+    act = torch.empty((1, I), dtype=torch.float16, device=dev)
+    y = torch.empty((1, H), dtype=torch.float16, device=dev)
+    for r in range(2 * sets):
+        layers[r % sets].gate_up(x, act)
+    torch.cuda.synchronize()
+    log(f"pmc probe: {2 * sets} gate_up launches (M=1)")
+    for r in range(2 * sets):
+        layers[r % sets].down(act, y)
+    torch.cuda.synchronize()
+    log(f"pmc probe: {2 * sets} down launches (M=1)")
 
 
 def cpu_baseline(seconds, h, i, label):
@@ -201,6 +262,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--quick", action="store_true", help="headline decode only")
     ap.add_argument("--sets", type=int, default=6, help="weight sets rotated per decode step")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only launch the calibration copy and the headline GEMVs (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -216,6 +279,10 @@ def main():
     torch.cuda.set_device(dev)
     H, I, G = 4096, 14336, 128
     out = {}
+
+    if args.pmc_probe:
+        pmc_probe(hm, torch, dev, H, I, G, args.sets)
+        return
 
     log("building weight sets ...")
     layers = make_layers(hm, torch, dev, H, I, G, args.sets)
@@ -241,7 +308,7 @@ def main():
     achieved = gu_bytes / gu_sec / 1e9
     out["roofline"] = {"kernel": "gemv_kernel<F16, 1, 128, fused> (gate_up + SwiGLU, M=1)", "bound": "hbm",
                        "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                       "traffic": None, "avg_launch_us": round(gu_sec * 1e6, 3), "algorithmic_bytes_per_launch": gu_bytes}
+                       "traffic": measured_traffic(), "avg_launch_us": round(gu_sec * 1e6, 3), "algorithmic_bytes_per_launch": gu_bytes}
     log(f"gate_up kernel: {gu_sec * 1e6:.2f} us, {achieved:.1f} GB/s")
 
     extra = {}
