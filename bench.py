@@ -1,13 +1,12 @@
 #!/usr/bin/env python3
-"""W4A16 SwiGLU FFN benchmark on one MI355X (BASELINE.json metric: decode GB/s and prefill TFLOP/s at the
-Llama-3-8B FFN shape).
+"""W4A16 SwiGLU FFN benchmark on one MI355X: decode GB/s and prefill TFLOP/s at the Llama-3-8B FFN shape.
 
-Headline `value`: Llama-3-8B FFN layer decode, M = 1, fp16 activations, W4A16 group 128 (BASELINE config 2),
+Headline `value`: Llama-3-8B FFN layer decode, M = 1, fp16 activations, W4A16 group 128,
 as algorithmic GB/s (weights + x + y per layer, inputs resident in HBM). A step is one FFN layer pass over one
 batch. Six independent weight sets (553 MB) rotate so the 256 MB Infinity Cache cannot serve the weights.
 The steps are captured in a HIP graph and replayed, so host launch overhead is not timed.
-Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), the 32-layer decode stack
-(config 4), the Qwen2.5-14B g = 64 shape (config 5), a per-kernel roofline for the dominant kernel measured
+Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), a 32-layer decode stack with
+RMSNorm and residual between layers, the Qwen2.5-14B g = 64 shape, a per-kernel roofline for the dominant kernel measured
 with HIP events, and the reference CPU path (restated AVX-512 GEMV) timed on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
@@ -328,7 +327,7 @@ def main():
     torch.cuda.empty_cache()
 
     if not args.quick:
-        # BASELINE config 4: 32 distinct layers, RMSNorm (eps 1e-5) + residual between layers, decode M = 1.
+        # 32 distinct layers, RMSNorm (eps 1e-5) + residual between layers, decode M = 1.
         stack = make_layers(hm, torch, dev, H, I, G, 32, seed=1)
         x = torch.randn((1, H), device=dev).to(torch.float16)
         normed, y = torch.empty_like(x), torch.empty_like(x)
@@ -353,7 +352,7 @@ def main():
         del stack, gt
         torch.cuda.empty_cache()
 
-        # BASELINE config 5: Qwen2.5-14B FFN shape, group 64.
+        # Qwen2.5-14B FFN shape, group 64.
         qh, qi, qg = 5120, 13824, 64
         ql = make_layers(hm, torch, dev, qh, qi, qg, 4, seed=2)
         s, _, _ = decode_bench(hm, torch, dev, ql, 1, qh, args.steps, args.warmup)

@@ -98,8 +98,8 @@ hm_status hm_weights_from_tiles(const uint8_t *tiles, int64_t packed_k, int64_t 
 
 /* From logical device tensors: q [K, N] uint8 (0..15), scales [K/group, N]
  * (dtype bits), zeros [K/group, N] uint8 (0..15), row-major. group in
- * {32, 64, 128}. Covers what the 4352-byte layout cannot hold (group 64,
- * SURVEY finding: packers drop the second group of each tile). */
+ * {32, 64, 128}. Covers what the 4352-byte layout cannot hold: a tile stores one
+ * scale/zero row per 128 K rows, so group 64 or 32 weights need this entry. */
 hm_status hm_weights_from_logical(const uint8_t *q, const uint16_t *scales, const uint8_t *zeros, int64_t K,
                                   int64_t N, int64_t group, hm_dtype dtype, void *stream, hm_weights **out);
 

@@ -142,7 +142,7 @@ def dequantize(q, scales, zeros, group):
 
 
 def random_weights(rng, k, n, group, dtype, s_lo=0.001, s_hi=0.02, z_lo=0, z_hi=16):
-    """Seeded W4A16 weights with BASELINE's distributions: q uniform 0..15, scales U(s_lo, s_hi) rounded to
+    """Seeded W4A16 weights with the benchmark distributions: q uniform 0..15, scales U(s_lo, s_hi) rounded to
     `dtype` (bits), zeros uniform z_lo..z_hi-1."""
     q = rng.integers(0, 16, (k, n), dtype=np.uint8)
     s = to_bits(rng.uniform(s_lo, s_hi, (k // group, n)).astype(np.float32), dtype)

@@ -6,7 +6,7 @@ import ctypes
 import numpy as np
 import torch
 
-# North-star bar for fp16 output: max|got-ref| / max|ref| <= 1e-2 and relative L2 <= 1e-3.
+# Parity bar for fp16 output: max|got-ref| / max|ref| <= 1e-2 and relative L2 <= 1e-3.
 # bf16 output carries one bf16 rounding (~1.7e-3 rel-L2 by itself), so it uses the reference's own bar for a
 # result with one bf16 rounding (kernels/gpu/tests/test_gpu_ffn.cpp:34): rel-L2 <= 5e-3.
 TOL = {

@@ -1,4 +1,4 @@
-"""GPU: the SwiGLU FFN layer (fused gate_up + SiLU*up, then down) against the float64 oracle at BASELINE's
+"""GPU: the SwiGLU FFN layer (fused gate_up + SiLU*up, then down) against the float64 oracle at the benchmark's
 shapes, the channel and row partitions, the GpuFfnModel mirror, and the elementwise operators."""
 
 import numpy as np
@@ -13,7 +13,7 @@ _CACHE = {}
 
 
 def _layer(oracle, hm, device, hidden, inter, group, dtype, seed):
-    """Seeded layer (BASELINE distributions: q, z uniform 0..15, s ~ U(0.001, 0.02)), cached per shape."""
+    """Seeded layer (benchmark distributions: q, z uniform 0..15, s ~ U(0.001, 0.02)), cached per shape."""
     key = (hidden, inter, group, dtype, seed)
     if key not in _CACHE:
         _CACHE.clear()
@@ -81,7 +81,7 @@ def test_ffn_qwen14b_group64(oracle, hm, device):
 
 @pytest.mark.parametrize("m", [1, 1024])
 def test_partition_channel_split_qwen(oracle, hm, device, m):
-    # GPU share 75% (10368 channels) and 25% (3456), run one after the other on the GPU,
+    # Qwen2.5-14B shape: GPU share 75% (10368 channels) and 25% (3456), run one after the other on the GPU,
     # summed, against the unsplit layer and the oracle.
     layer, _, wf = _layer(oracle, hm, device, 5120, 13824, 64, "fp16", 2)
     part = hm.FFNPartition.from_ratio(13824, 0.25)
@@ -227,7 +227,7 @@ def test_rmsnorm_and_residuals(oracle, hm, device, dtype):
 
 
 def test_ffn_stack_decode_small(oracle, hm, device):
-    # BASELINE config 4 semantics on a small stack: per layer normed = RMSNorm(x); x += FFN(normed).
+    # Layer-stack semantics on a small stack: per layer normed = RMSNorm(x); x += FFN(normed).
     rng = np.random.default_rng(99)
     hidden, inter, layers, steps, dtype = 512, 1536, 4, 3, "fp16"
     model = hm.GpuFfnModel(torch.float16)
