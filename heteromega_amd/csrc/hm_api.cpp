@@ -119,31 +119,6 @@ hm_status check_logical(const uint8_t *q, const uint16_t *s, const uint8_t *z, i
 // Rows beyond this use the MFMA GEMM; up to it, the decode GEMV.
 constexpr int64_t kGemvMaxRows = 16;
 
-// Waves per decode-GEMV workgroup. HM_GEMV_FUSED_WAVES / HM_GEMV_PLAIN_WAVES override the defaults (tuning).
-int env_int(const char *name, int fallback) {
-    const char *v = std::getenv(name);
-    return v != nullptr && *v != '\0' ? std::atoi(v) : fallback;
-}
-
-// Enough waves that each holds at most one batch of tiles (16, or 8 for group 32), between 4 and 16 waves.
-int gemv_waves(int64_t kt_count, bool fused, int64_t group) {
-    static const int fused_waves = env_int("HM_GEMV_FUSED_WAVES", 0);
-    static const int plain_waves = env_int("HM_GEMV_PLAIN_WAVES", 0);
-    if (fused && fused_waves > 0) {
-        return fused_waves;
-    }
-    if (!fused && plain_waves > 0) {
-        return plain_waves;
-    }
-    const int64_t batch = group >= 64 ? 16 : 8;
-    const int64_t tiles = fused ? 2 * kt_count : kt_count;
-    int waves = 4;
-    while (waves < 16 && tiles > waves * batch) {
-        waves *= 2;
-    }
-    return waves;
-}
-
 hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t strip_begin,
                      int64_t n, int64_t kt_begin, int64_t kt_count, bool fused, void *workspace, size_t workspace_bytes,
                      hipStream_t stream) {
@@ -160,9 +135,7 @@ hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, i
         c.kt_begin = kt_begin;
         c.kt_count = kt_count;
         c.fused = fused;
-        c.waves = gemv_waves(kt_count, fused, p.group);
-        c.splits = hm::gemv_pick_splits(c);
-        const size_t need = hm::gemv_partial_bytes(c);
+        const size_t need = hm::plan_gemv(c).partial_bytes;
         if (need > workspace_bytes) {
             return fail(HM_WORKSPACE_TOO_SMALL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
         }
@@ -201,8 +174,7 @@ size_t linear_workspace(const hm::Planes &p, int64_t M, int64_t n, int64_t kt_co
     c.n = n;
     c.kt_count = kt_count;
     c.fused = fused;
-    c.waves = gemv_waves(kt_count, fused, p.group);
-    return hm::gemv_partial_bytes(c);
+    return hm::plan_gemv(c).partial_bytes;
 }
 
 hm_status check_activation(const void *x, int64_t ldx, int64_t width, const char *what) {
@@ -567,6 +539,7 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
     size_t partial = 0;
     for (int64_t m = 1; m <= std::min<int64_t>(max_m, kGemvMaxRows); ++m) {
         partial = std::max(partial, linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false));
+        partial = std::max(partial, linear_workspace(f->gate_up.p, m, f->inter, f->hidden / 128, true));
     }
     return act + partial;
 }

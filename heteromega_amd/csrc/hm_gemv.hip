@@ -1,98 +1,120 @@
 // Decode W4A16 GEMV for M <= 16 rows on the strip layout, with an optional fused SwiGLU epilogue.
 //
-// Work split. Workgroup = `waves` wave64s over one unit: one strip (16 columns) or, fused, a strip pair
-// (gate and up of the same 16 channels). The unit's K tiles are dealt to its waves round-robin. A wave reads
-// one 1 KiB strip tile per step with one 16-byte load per lane, so each wave load instruction is fully
-// coalesced. A wave requests its tiles in batches of up to 16 (one memory round trip per batch), after the
-// activation chunks that the workgroup stages in LDS.
+// Work split. A wave owns S strips (S = 2: the gate and up strips of 16 channels when fused, or two adjacent
+// strips) over a contiguous run of the K tiles of its split; `wps` waves share a strip group's K range and add
+// their partial sums through LDS at the end. A workgroup holds `nu` strip groups over one K range (split), so
+// the activation chunk it stages in LDS once serves nu * S strips: for M > 1 that chunk is M times larger
+// than for one row, and sharing it is what keeps its L2 -> LDS traffic below the weight traffic. Splits only
+// bound the staged chunk (64 KiB); their fp32 partials are added by sum_splits, which applies SwiGLU when
+// fused.
+//
+// Streaming. Each wave keeps a ring of KB steps (S strip tiles and their scale/zero records per step) in
+// flight: the tile of step i + KB is requested as soon as step i has consumed its registers, and each step
+// waits only for its own loads (in-order vmcnt). A strip tile is 1 KiB read with one 16-byte load per lane,
+// so every wave load is fully coalesced; weights use non-temporal loads. A ring of 8 tiles per wave keeps
+// the register count near 100, so four or more waves fit per SIMD and every workgroup of a decode launch is
+// resident at once (the launch streams without a second round of workgroups).
 //
 // Math per strip tile (4 MFMA steps of 32 K): the B operand is bias + q straight from the nibbles
-// (hm_device.hpp), A is the activation rows from LDS (rows >= m are zero), so
+// (hm_device.hpp), A is the activation rows from LDS, so
 //   P = sum_k x'_k (bias + q'_k)       (q' = q, or 16 q on the fp16 odd pairs with x' = x / 16)
 //     = sum_k x_k q_k + Xb,            Xb = bias * sum_k x'_k
 // and per group, with scale s and zero z of the column, sum_k x_k (q_k - z) s = s (P - Xb - z X), X = sum_k x_k.
 // Xb and X per (row, group) are computed once when the workgroup stages x. This is the reference's
 // per-tile factorization s (sum q x - z sum x) (kernels/gpu/src/gemv_w4a16.cu:91-98,
-// src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:242-253), applied to MFMA partial sums.
+// src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:242-253), applied to MFMA partial sums. One LDS read of an
+// A fragment feeds the MFMAs of all S strips.
 //
-// Output: the waves of a strip add their partials through LDS. Plain: y = round(sum) or an fp32 partial for
-// split-K. Fused: act = round(SiLU(gate) * up), fp32 math, one rounding (kernels/gpu/src/silu_mul.cu:10-30).
+// Output: plain y = round(sum), fused act = round(SiLU(gate) * up) with fp32 math and one rounding
+// (kernels/gpu/src/silu_mul.cu:10-30), or fp32 partials per split.
 #include "hm_device.hpp"
 #include "hm_internal.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace hm {
 namespace {
 
-
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr size_t kXBudget = 64 * 1024; // staged activation bytes per workgroup (bounds the K range of a split)
 
 struct GemvArgs {
     const uint4 *quant;
     const uint32_t *meta;
     const uint16_t *x;
     uint16_t *y;
-    float *partial;
+    float *partial; // [splits][m][ncols] fp32, or nullptr when the call has one split
     int64_t ldx, ldy;
     int kt_pitch;
     int kt_begin, kt_count, kt_per_split;
-    int strip_begin;
+    int strip_begin; // first strip of the call
+    int groups;      // strip groups (S strips each) of the call
     int m;
-    int n; // output columns or channels (row length of `partial`)
+    int ncols; // 16 * strips of the call (row length of `partial`)
+    int nu;    // strip groups per workgroup
+    int wps;   // waves per strip group
 };
 
-// Dynamic LDS: xs [m][KC] 16-bit, sums [m][KC / G] float2 (Xb, X), red [waves][m][16] float.
-template <class T, int MT, int G, bool FUSED, int WGS>
-__global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
+// Dynamic LDS: xs [m][kc + 8] 16-bit, sums [m][kc / G + 1] float2 (Xb, X); after the multiply the front of
+// the same space holds red [waves][S][m][16] float.
+template <class T, int MT, int G, int S, bool FUSED, int WGS>
+__global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int NS = FUSED ? 2 : 1;
-    constexpr int ROWS = MT < 4 ? MT : 4; // D elements per lane that can hold a real row
-    constexpr int GPT = 128 / G;          // groups per strip tile
-    constexpr int SPG = 4 / GPT;          // MFMA steps per group
-    constexpr int KB = G >= 64 ? 16 : 8;  // weight tiles per wave per batch
+    constexpr int ROWS = MT == 1 ? 1 : 4; // D elements per lane that can hold a real row
+    constexpr int GPT = 128 / G;           // groups per strip tile
+    constexpr int SPG = 4 / GPT;           // MFMA steps per group
+    // Ring depth in steps: 8 tiles in flight per wave, fewer where the records (group < 128) and the
+    // four-row folds (M > 1) need the registers.
+    constexpr int kInFlight = (MT > 1 && (S == 1 || GPT > 1)) ? 4 : 8; // strip tiles
+    constexpr int KB = kInFlight / S / (GPT == 4 ? 2 : 1) > 0 ? kInFlight / S / (GPT == 4 ? 2 : 1) : 1;
+    constexpr int CPG = G / 8;             // 8-element activation chunks per group
+    constexpr int kPre = 4;                // chunks per thread fetched ahead of the weights
 
     const int tid = threadIdx.x;
-    const int waves = WGS / 64;
     const int wave = uniform(tid >> 6);
     const int lane = tid & 63;
     const int m = a.m;
+    const int col = lane & 15;
+    const int h = lane >> 4;
 
     const int split = blockIdx.y;
     const int kt0 = a.kt_begin + split * a.kt_per_split;
     const int nkt = min(a.kt_per_split, a.kt_begin + a.kt_count - kt0);
-    const int kc = nkt * 128;       // K values of this split
-    const int kg = kc / G;          // groups of this split
+    const int kc = nkt * 128; // K values of this split
+    const int kg = kc / G;    // groups of this split
     const int64_t xk0 = static_cast<int64_t>(kt0 - a.kt_begin) * 128;
 
     // Row strides padded by 16 bytes (x) and 8 bytes (sums) so that lanes reading different rows of one MFMA
     // operand or fold hit different LDS banks.
-    const int xst = kc + 8;  // staged row stride, 16-bit elements
-    const int sst = kg + 1;  // sums row stride, float2
+    const int xst = kc + 8;
+    const int sst = kg + 1;
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
     float2 *sums = reinterpret_cast<float2 *>(smem + static_cast<size_t>(m) * xst * 2);
-    float *red = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(sums) + static_cast<size_t>(m) * sst * sizeof(float2));
+    float *red = reinterpret_cast<float *>(smem);
 
-    // Tile stream of this wave: strip `strip`, a contiguous run of its local tiles.
-    const int wps = waves / NS;          // waves per strip
-    const int j = FUSED ? (wave & 1) : 0; // strip of this wave within the unit
-    const int wi = FUSED ? (wave >> 1) : wave;
-    const int strip = a.strip_begin + blockIdx.x * NS + j;
-    const uint4 *qp = a.quant + (static_cast<int64_t>(strip) * a.kt_pitch + kt0) * 64; // wave-uniform base
-    const int col = lane & 15;
-    const int h = lane >> 4;
-    const uint32_t *mp = a.meta + ((static_cast<int64_t>(strip) * a.kt_pitch + kt0) * 16 + col) * GPT;
-    // Each wave of a strip takes a contiguous run of tiles [tb, te).
-    const int tpw = (nkt + wps - 1) / wps;
+    // This wave's strip group and its contiguous run [tb, te) of the split's tiles. Groups past the end of
+    // the call (a partial last workgroup) read the last group and are not stored.
+    const int grp = wave % a.nu;
+    const int wi = wave / a.nu;
+    const int gidx = min(static_cast<int>(blockIdx.x) * a.nu + grp, a.groups - 1);
+    const int strip0 = a.strip_begin + gidx * S;
+    const uint4 *qp[S];
+    const uint32_t *mp[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int64_t tile0 = static_cast<int64_t>(strip0 + s) * a.kt_pitch + kt0;
+        qp[s] = a.quant + tile0 * 64;
+        mp[s] = a.meta + (tile0 * 16 + col) * GPT;
+    }
+    const int tpw = (nkt + a.wps - 1) / a.wps;
     const int tb = wi * tpw;
     const int te = min(tb + tpw, nkt);
+    const int last = te - 1; // >= 0: a wave past the split's end gets te = nkt >= 1 and reads only zero-weighted tiles
 
-    // Memory requests go out in this order: the activation chunks this thread stages (up to kPre, held in
-    // registers), then the wave's whole first batch of weight tiles and records. Staging then waits for the
-    // activations only, so it costs one round trip and never waits for the weights. (LDS DMA loads would
-    // save the registers, but the compiler then waits for vmcnt(0) before every LDS read.)
-    constexpr int CPG = G / 8;              // 8-element activation chunks per group
-    constexpr int kPre = MT == 1 ? 4 : 8;   // chunks per thread staged ahead of the weights
+    // Memory requests go out in this order: the activation chunks this thread stages (held in registers),
+    // then the first KB steps of the wave's ring. Staging waits for the activations only.
     const int chunks_row = kc / 8;
     const int total = m * chunks_row;
     uint4 xv[kPre];
@@ -106,40 +128,37 @@ __global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
     };
     fetch(0);
 
-    // A batch is KB consecutive tiles from i0. Indices past the wave's run are clamped to its last tile, so
-    // the batch has no branches and the compiler can wait for each tile's loads separately (s_waitcnt vmcnt
-    // counting down) instead of for all of them; the clamped copies are weighted by zero.
-    uint4 wq[KB];
-    uint32_t rq[KB][GPT];
-    // The small record loads go first: folds then wait for them without waiting for the weight tiles.
-    auto load = [&](int i0) {
+    uint4 wq[KB][S];
+    uint32_t rq[KB][S][GPT];
+    // Step u of the ring <- local tile i (already clamped to [0, last]): records first, then the weights.
+    auto load = [&](int u, int i) {
 #pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int i = max(min(i0 + u, te - 1), 0); // a wave without tiles loads tile te - 1 >= 0 and skips it
+        for (int s = 0; s < S; ++s) {
             if constexpr (GPT == 1) {
-                rq[u][0] = mp[i * 16];
+                rq[u][s][0] = mp[s][i * 16];
             } else if constexpr (GPT == 2) {
-                const uint2 r = *reinterpret_cast<const uint2 *>(mp + i * 32);
-                rq[u][0] = r.x;
-                rq[u][1] = r.y;
+                const uint2 r = *reinterpret_cast<const uint2 *>(mp[s] + i * 32);
+                rq[u][s][0] = r.x;
+                rq[u][s][1] = r.y;
             } else {
-                const uint4 r = *reinterpret_cast<const uint4 *>(mp + i * 64);
-                rq[u][0] = r.x;
-                rq[u][1] = r.y;
-                rq[u][2] = r.z;
-                rq[u][3] = r.w;
+                const uint4 r = *reinterpret_cast<const uint4 *>(mp[s] + i * 64);
+                rq[u][s][0] = r.x;
+                rq[u][s][1] = r.y;
+                rq[u][s][2] = r.z;
+                rq[u][s][3] = r.w;
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int i = max(min(i0 + u, te - 1), 0);
-            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(qp + i * 64 + lane));
-            wq[u] = uint4{v.x, v.y, v.z, v.w};
+        for (int s = 0; s < S; ++s) {
+            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(qp[s] + i * 64 + lane));
+            wq[u][s] = uint4{v.x, v.y, v.z, v.w};
         }
-        __builtin_amdgcn_sched_barrier(0);
     };
-    load(tb);
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+        load(u, min(tb + u, last));
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     // 1. Stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes take
     //    consecutive 8-element chunks of a row, so one group is G / 8 consecutive lanes.
@@ -183,123 +202,164 @@ __global__ void __launch_bounds__(WGS) gemv_kernel(GemvArgs a) {
         stage(idx, xv[c], idx < total); // all lanes take part in the shuffles
     }
     for (int base = kPre * WGS; base < total; base += kPre * WGS) {
-        fetch(base); // large M only: these chunks wait behind the weight batch
+        fetch(base); // large M only: these chunks wait behind the first ring steps
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
             const int idx = base + c * WGS + tid;
             stage(idx, xv[c], idx < total);
         }
     }
-    lds_barrier(); // not __syncthreads(): its fence would wait for the weight batch too
+    lds_barrier(); // not __syncthreads(): its fence would wait for the ring's loads too
 
-    // 2. Multiply.
-    // A-operand row of this lane. Rows >= m read row m - 1 instead of zeros: they only feed D rows >= m,
-    // which are never stored.
-    const int arow = min(lane & 15, m - 1);
+    // 2. Multiply. A-operand row of this lane: rows >= m read row m - 1 instead; they only feed D rows >= m,
+    //    which are never stored.
+    const int arow = min(col, m - 1);
     const uint16_t *xa = xs + arow * xst + 8 * h;
     const MagicRegs magic = magic_regs<T>();
 
-    float acc[ROWS];
-#pragma unroll
-    for (int e = 0; e < ROWS; ++e) {
-        acc[e] = 0.0f;
-    }
-    int srow[ROWS]; // rows of the D elements, clamped to a staged row
+    float acc[S][ROWS];
+    int srow[ROWS]; // staged rows of this lane's D elements
 #pragma unroll
     for (int e = 0; e < ROWS; ++e) {
         srow[e] = min(4 * h + e, m - 1);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            acc[s][e] = 0.0f;
+        }
     }
 
-    auto compute = [&](int i0) {
+    // One step: the S tiles of local tile i (unclamped: tiles past the wave's run are weighted by zero).
+    auto step = [&](int u, int i) {
+        const int ic = min(i, last);
+        const float live = i < te ? 1.0f : 0.0f;
+        float4_t p[S];
 #pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int i = min(i0 + u, te - 1);
-            const float live = (i0 + u < te) ? 1.0f : 0.0f;
-            const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
-            float4_t p = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int mu = 0; mu < 4; ++mu) {
+            const uint4 av = *reinterpret_cast<const uint4 *>(xa + ic * 128 + 32 * mu);
 #pragma unroll
-            for (int mu = 0; mu < 4; ++mu) {
-                const uint4 av = *reinterpret_cast<const uint4 *>(xa + i * 128 + 32 * mu);
-                const uint4 bv = magic_operand<T>(words[mu], magic);
+            for (int s = 0; s < S; ++s) {
+                const uint32_t word = mu == 0 ? wq[u][s].x : mu == 1 ? wq[u][s].y : mu == 2 ? wq[u][s].z : wq[u][s].w;
                 if (mu % SPG == 0) {
-                    p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    p[s] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 }
-                p = T::mfma16(av, bv, p);
-                if (mu % SPG == SPG - 1) {
-                    const int g = mu / SPG;
-                    const uint32_t rr = rq[u][g];
-                    const float s = T::to_float(rr & 0xFFFFu) * live;
+                p[s] = T::mfma16(av, magic_operand<T>(word, magic), p[s]);
+            }
+            if (mu % SPG == SPG - 1) {
+                const int g = mu / SPG;
+                const int gl = ic * GPT + g; // local group index
+                float2 xsum[ROWS];
+#pragma unroll
+                for (int e = 0; e < ROWS; ++e) {
+                    xsum[e] = sums[srow[e] * sst + gl];
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const uint32_t rr = rq[u][s][g];
+                    const float sc = T::to_float(rr & 0xFFFFu) * live;
                     const float z = static_cast<float>((rr >> 16) & 0xFFu);
-                    const int gl = i * GPT + g; // local group index
 #pragma unroll
                     for (int e = 0; e < ROWS; ++e) {
-                        const float2 xsum = sums[srow[e] * sst + gl];
-                        const float t = __builtin_fmaf(-z, xsum.y, p[e] - xsum.x);
-                        acc[e] = __builtin_fmaf(s, t, acc[e]);
+                        const float t = __builtin_fmaf(-z, xsum[e].y, p[s][e] - xsum[e].x);
+                        acc[s][e] = __builtin_fmaf(sc, t, acc[s][e]);
                     }
                 }
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
 
-    for (int i0 = tb; i0 < te; i0 += KB) {
-        compute(i0);
-        if (i0 + KB < te) {
-            load(i0 + KB);
+    const int rounds = (tpw + KB - 1) / KB; // the same for every wave of the workgroup
+    for (int r = 0; r + 1 < rounds; ++r) {
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int i = tb + r * KB + u;
+            step(u, i);
+            load(u, min(i + KB, last));
         }
     }
-
-    // 3. Add the waves of each strip, then write.
 #pragma unroll
-    for (int e = 0; e < ROWS; ++e) {
-        const int row = 4 * h + e;
-        if (row < m) {
-            red[(wave * m + row) * 16 + col] = acc[e];
+    for (int u = 0; u < KB; ++u) {
+        step(u, tb + (rounds - 1) * KB + u);
+    }
+
+    // 3. Add the waves of each strip group (red reuses the staging space), then write.
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int e = 0; e < ROWS; ++e) {
+            const int row = 4 * h + e;
+            if (row < m) {
+                red[((wave * S + s) * m + row) * 16 + col] = acc[s][e];
+            }
         }
     }
     __syncthreads();
-    for (int o = tid; o < m * 16; o += WGS) {
-        const int row = o >> 4;
+    constexpr int OUT_S = FUSED ? 1 : S; // outputs per (group, row, column)
+    const int outs = a.nu * OUT_S * m * 16;
+    for (int o = tid; o < outs; o += WGS) {
         const int c = o & 15;
-        float v[NS];
+        int rest = o >> 4;
+        const int row = rest % m;
+        rest /= m;
+        const int s_out = rest % OUT_S;
+        const int g = rest / OUT_S;
+        const int gg = static_cast<int>(blockIdx.x) * a.nu + g;
+        if (gg >= a.groups) {
+            continue;
+        }
+        float v[S];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
+        for (int s = 0; s < S; ++s) {
             float t = 0.0f;
-            for (int w = 0; w < wps; ++w) {
-                t += red[((w * NS + s) * m + row) * 16 + c];
+            for (int w = 0; w < a.wps; ++w) {
+                t += red[(((w * a.nu + g) * S + s) * m + row) * 16 + c];
             }
             v[s] = t;
         }
-        const int out_col = blockIdx.x * 16 + c;
-        if constexpr (FUSED) {
-            a.y[row * a.ldy + out_col] = T::from_float(silu(v[0]) * v[1]);
-        } else if (a.partial != nullptr) {
-            a.partial[(static_cast<int64_t>(split) * m + row) * a.n + out_col] = v[0];
+        if (a.partial != nullptr) {
+            float *pr = a.partial + (static_cast<int64_t>(split) * m + row) * a.ncols + gg * S * 16 + c;
+            if constexpr (FUSED) {
+                pr[0] = v[0];
+                pr[16] = v[1];
+            } else {
+                pr[s_out * 16] = v[s_out];
+            }
+        } else if constexpr (FUSED) {
+            a.y[row * a.ldy + gg * 16 + c] = T::from_float(silu(v[0]) * v[1]);
         } else {
-            a.y[row * a.ldy + out_col] = T::from_float(v[0]);
+            a.y[row * a.ldy + (gg * S + s_out) * 16 + c] = T::from_float(v[s_out]);
         }
     }
 }
 
-template <class T>
+// Adds the split partials [splits][m][ncols]; fused: ncols alternate gate and up per 16 columns and the
+// output is SiLU(gate) * up per channel (ncols / 2 channels).
+template <class T, bool FUSED>
 __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ partial, uint16_t *__restrict__ y, int64_t ldy, int m,
-                                                  int n, int splits) {
+                                                  int ncols, int splits) {
+    const int nout = FUSED ? ncols / 2 : ncols;
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= static_cast<int64_t>(m) * n) {
+    if (idx >= static_cast<int64_t>(m) * nout) {
         return;
     }
-    const int row = static_cast<int>(idx / n);
-    const int c = static_cast<int>(idx - static_cast<int64_t>(row) * n);
-    float v = 0.0f;
+    const int row = static_cast<int>(idx / nout);
+    const int c = static_cast<int>(idx - static_cast<int64_t>(row) * nout);
+    const int cg = FUSED ? (c >> 4) * 32 + (c & 15) : c; // gate (or plain) column
+    float g = 0.0f, u = 0.0f;
     for (int s = 0; s < splits; ++s) {
-        v += partial[(static_cast<int64_t>(s) * m + row) * n + c];
+        const float *pr = partial + (static_cast<int64_t>(s) * m + row) * ncols + cg;
+        g += pr[0];
+        if constexpr (FUSED) {
+            u += pr[16];
+        }
     }
-    y[row * ldy + c] = T::from_float(v);
+    y[row * ldy + c] = T::from_float(FUSED ? silu(g) * u : g);
 }
 
-template <class T, int MT, int G, bool FUSED, int WGS>
+template <class T, int MT, int G, int S, bool FUSED, int WGS>
 hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
-    auto kern = gemv_kernel<T, MT, G, FUSED, WGS>;
+    auto kern = gemv_kernel<T, MT, G, S, FUSED, WGS>;
     static bool configured = false; // one attribute call per instantiation
     if (!configured) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -312,116 +372,140 @@ hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Fused (gate/up pairs) runs 4 or 8 waves per workgroup, plain 4, 8 or 16.
-template <class T, int MT, int G> hipError_t launch_g(const GemvArgs &a, bool fused, dim3 grid, int threads, size_t lds, hipStream_t s) {
-    if (fused) {
-        return threads >= 512 ? launch_w<T, MT, G, true, 512>(a, grid, lds, s) : launch_w<T, MT, G, true, 256>(a, grid, lds, s);
+template <class T, int MT, int G, int S, bool FUSED>
+hipError_t launch_s(const GemvArgs &a, dim3 grid, int waves, size_t lds, hipStream_t s) {
+    switch (waves) {
+    case 4:
+        return launch_w<T, MT, G, S, FUSED, 256>(a, grid, lds, s);
+    case 8:
+        return launch_w<T, MT, G, S, FUSED, 512>(a, grid, lds, s);
+    default:
+        return launch_w<T, MT, G, S, FUSED, 1024>(a, grid, lds, s);
     }
-    if constexpr (G == 128 && MT == 1) { // other shapes need more registers than 16 waves per CU allow
-        if (threads >= 1024) {
-            return launch_w<T, MT, G, false, 1024>(a, grid, lds, s);
-        }
-    }
-    return threads >= 512 ? launch_w<T, MT, G, false, 512>(a, grid, lds, s) : launch_w<T, MT, G, false, 256>(a, grid, lds, s);
 }
 
-template <class T, int MT> hipError_t launch_m(const GemvArgs &a, int group, bool fused, dim3 grid, int threads, size_t lds, hipStream_t s) {
+template <class T, int MT, int G>
+hipError_t launch_g(const GemvArgs &a, bool fused, int strips_per_wave, dim3 grid, int waves, size_t lds, hipStream_t s) {
+    if (fused) {
+        return launch_s<T, MT, G, 2, true>(a, grid, waves, lds, s);
+    }
+    if (strips_per_wave == 2) {
+        return launch_s<T, MT, G, 2, false>(a, grid, waves, lds, s);
+    }
+    return launch_s<T, MT, G, 1, false>(a, grid, waves, lds, s);
+}
+
+template <class T, int MT>
+hipError_t launch_m(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, size_t lds, hipStream_t s) {
     switch (group) {
     case 32:
-        return launch_g<T, MT, 32>(a, fused, grid, threads, lds, s);
+        return launch_g<T, MT, 32>(a, fused, spw, grid, waves, lds, s);
     case 64:
-        return launch_g<T, MT, 64>(a, fused, grid, threads, lds, s);
+        return launch_g<T, MT, 64>(a, fused, spw, grid, waves, lds, s);
     default:
-        return launch_g<T, MT, 128>(a, fused, grid, threads, lds, s);
+        return launch_g<T, MT, 128>(a, fused, spw, grid, waves, lds, s);
     }
 }
 
-template <class T> hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, dim3 grid, int threads, size_t lds, hipStream_t s) {
-    if (a.m <= 1) {
-        return launch_m<T, 1>(a, group, fused, grid, threads, lds, s);
-    }
-    if (a.m <= 4) {
-        return launch_m<T, 4>(a, group, fused, grid, threads, lds, s);
-    }
-    return launch_m<T, 16>(a, group, fused, grid, threads, lds, s);
+template <class T>
+hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, size_t lds, hipStream_t s) {
+    return a.m <= 1 ? launch_m<T, 1>(a, group, fused, spw, grid, waves, lds, s) : launch_m<T, 16>(a, group, fused, spw, grid, waves, lds, s);
 }
 
-constexpr size_t kLdsBudget = 96 * 1024;
+int env_int(const char *name) {
+    const char *v = std::getenv(name);
+    return v != nullptr ? std::atoi(v) : 0;
+}
 
 } // namespace
 
-namespace {
-// Waves per workgroup that a launch uses for c.waves.
-int effective_waves(const GemvCall &c) {
-    if (c.fused) {
-        return c.waves >= 8 ? 8 : 4;
+GemvPlan plan_gemv(const GemvCall &c) {
+    GemvPlan p;
+    const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
+    p.spw = c.fused ? 2 : (c.m > 1 && strips % 2 == 0 ? 2 : 1);
+    p.groups = strips / p.spw;
+    // K split: the staged activation chunk stays within kXBudget.
+    const int64_t max_tiles = std::max<int64_t>(1, static_cast<int64_t>(kXBudget) / (c.m * 256));
+    const int64_t splits0 = (c.kt_count + max_tiles - 1) / max_tiles;
+    p.kt_per_split = (c.kt_count + splits0 - 1) / splits0;
+    p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
+    // Waves per strip group: up to 8, keeping at least 8 tiles per wave.
+    p.wps = 1;
+    while (p.wps < 8 && p.kt_per_split >= 16 * p.wps) {
+        p.wps *= 2;
     }
-    return (c.waves >= 16 && c.w.group == 128 && c.m == 1) ? 16 : c.waves >= 8 ? 8 : 4;
-}
-
-// LDS of one workgroup that stages kt_per_split K tiles.
-size_t lds_for(const GemvCall &c, int64_t kt_per_split) {
-    const int64_t kc = kt_per_split * 128;
-    const size_t xs = static_cast<size_t>(c.m) * (kc + 8) * 2;
-    const size_t sums = static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
-    const size_t red = static_cast<size_t>(effective_waves(c)) * c.m * 16 * sizeof(float);
-    return xs + sums + red;
-}
-} // namespace
-
-size_t gemv_lds_bytes(const GemvCall &c, int splits) { return lds_for(c, (c.kt_count + splits - 1) / splits); }
-
-int gemv_pick_splits(const GemvCall &c) {
-    if (c.fused) {
-        return 1; // the SwiGLU epilogue needs whole sums
+    // Strip groups per workgroup: at least 4 waves; with several rows, more groups share one staged chunk
+    // while the grid keeps at least one workgroup per CU.
+    p.nu = 1;
+    while (p.nu * p.wps < 4) {
+        p.nu *= 2;
     }
-    int splits = 1;
-    while (gemv_lds_bytes(c, splits) > kLdsBudget && splits < c.kt_count) {
-        ++splits;
+    if (c.m > 1) {
+        while (p.nu * p.wps < 16 && ((p.groups + 2 * p.nu - 1) / (2 * p.nu)) * p.splits >= 256) {
+            p.nu *= 2;
+        }
     }
-    return splits;
-}
-
-size_t gemv_partial_bytes(const GemvCall &c) {
-    const int splits = gemv_pick_splits(c);
-    return splits > 1 ? static_cast<size_t>(splits) * c.m * c.n * sizeof(float) : 0;
+    if (const int nu = env_int("HM_GEMV_NU")) { // tuning override
+        p.nu = nu;
+    }
+    if (const int wps = env_int("HM_GEMV_WPS")) {
+        p.wps = wps;
+    }
+    p.waves = p.nu * p.wps;
+    const int64_t kc = p.kt_per_split * 128;
+    const size_t stage = static_cast<size_t>(c.m) * (kc + 8) * 2 + static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
+    const size_t red = static_cast<size_t>(p.waves) * p.spw * c.m * 16 * sizeof(float);
+    p.lds = std::max(stage, red);
+    p.partial_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * c.m * strips * 16 * sizeof(float) : 0;
+    return p;
 }
 
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
+    const GemvPlan p = plan_gemv(c);
+    if (p.waves != 4 && p.waves != 8 && p.waves != 16) {
+        return hipErrorInvalidConfiguration;
+    }
     GemvArgs a;
     a.quant = reinterpret_cast<const uint4 *>(c.w.quant);
     a.meta = c.w.meta;
     a.x = c.x;
     a.y = c.y;
+    a.partial = p.splits > 1 ? c.partial : nullptr;
     a.ldx = c.ldx;
     a.ldy = c.ldy;
     a.kt_pitch = static_cast<int>(c.w.kt_pitch());
     a.kt_begin = static_cast<int>(c.kt_begin);
     a.kt_count = static_cast<int>(c.kt_count);
+    a.kt_per_split = static_cast<int>(p.kt_per_split);
     a.strip_begin = static_cast<int>(c.strip_begin);
+    a.groups = static_cast<int>(p.groups);
     a.m = static_cast<int>(c.m);
-    a.n = static_cast<int>(c.n);
-    const int splits = c.splits > 0 ? c.splits : 1;
-    a.kt_per_split = static_cast<int>((c.kt_count + splits - 1) / splits);
-    const int real_splits = static_cast<int>((c.kt_count + a.kt_per_split - 1) / a.kt_per_split);
-    a.partial = real_splits > 1 ? c.partial : nullptr;
-    const int units = static_cast<int>(c.n / 16);
-    const dim3 grid(units, real_splits);
-    const int threads = effective_waves(c) * 64;
-    const size_t lds = lds_for(c, a.kt_per_split);
+    a.ncols = static_cast<int>(p.groups * p.spw * 16);
+    a.nu = p.nu;
+    a.wps = p.wps;
+    const dim3 grid(static_cast<unsigned>((p.groups + p.nu - 1) / p.nu), static_cast<unsigned>(p.splits));
     const int group = static_cast<int>(c.w.group);
-    hipError_t e = c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, grid, threads, lds, stream)
-                                  : launch_dtype<BF16>(a, group, c.fused, grid, threads, lds, stream);
-    if (e != hipSuccess || real_splits == 1) {
+    hipError_t e = c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream)
+                                  : launch_dtype<BF16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream);
+    if (e != hipSuccess || p.splits == 1) {
         return e;
     }
     const int64_t total = c.m * c.n;
+    const dim3 blocks(static_cast<unsigned>((total + 255) / 256));
+    const int m = static_cast<int>(c.m);
+    const int splits = static_cast<int>(p.splits);
     if (c.w.dtype == 1) {
-        hipLaunchKernelGGL(sum_splits<F16>, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, c.partial, c.y,
-                           c.ldy, static_cast<int>(c.m), static_cast<int>(c.n), real_splits);
+        if (c.fused) {
+            hipLaunchKernelGGL((sum_splits<F16, true>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+        } else {
+            hipLaunchKernelGGL((sum_splits<F16, false>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+        }
     } else {
-        hipLaunchKernelGGL(sum_splits<BF16>, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, c.partial, c.y,
-                           c.ldy, static_cast<int>(c.m), static_cast<int>(c.n), real_splits);
+        if (c.fused) {
+            hipLaunchKernelGGL((sum_splits<BF16, true>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+        } else {
+            hipLaunchKernelGGL((sum_splits<BF16, false>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+        }
     }
     return hipGetLastError();
 }

@@ -51,13 +51,19 @@ struct GemvCall {
     int64_t n = 0; // output columns (plain) or channels (fused)
     int64_t kt_begin = 0, kt_count = 0;
     bool fused = false;
-    float *partial = nullptr; // split-K partials, [splits, m, n] fp32
-    int splits = 1;
-    int waves = 4;
+    float *partial = nullptr; // split-K partials (GemvPlan::partial_bytes)
 };
-size_t gemv_partial_bytes(const GemvCall &c);
-int gemv_pick_splits(const GemvCall &c);
-size_t gemv_lds_bytes(const GemvCall &c, int splits);
+// Launch shape of a GemvCall: strips per wave, strip groups, K split, waves per strip group, strip groups per
+// workgroup, LDS bytes and the fp32 partial buffer the split needs (0 without a split).
+struct GemvPlan {
+    int spw = 1;
+    int64_t groups = 0;
+    int64_t splits = 1, kt_per_split = 0;
+    int wps = 1, nu = 1, waves = 4;
+    size_t lds = 0;
+    size_t partial_bytes = 0;
+};
+GemvPlan plan_gemv(const GemvCall &c);
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream);
 
 // Prefill GEMM (MFMA 32x32x16) with the same operand conventions; fused writes SiLU(gate) * up.

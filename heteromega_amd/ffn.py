@@ -338,7 +338,9 @@ class FfnLayer:
         m = x.size(0)
         if act is None:
             act = torch.empty((m, e - b), dtype=x.dtype, device=x.device)
-        _call(_lib.load().hm_ffn_gate_up(self._h, _ptr(act), act.stride(0), _ptr(x), x.stride(0), m, b, e, ctypes.c_void_p(0), 0,
+        ws = self.workspace(m, stream)
+        wp, wb = _aligned(ws, self.workspace_bytes(m))
+        _call(_lib.load().hm_ffn_gate_up(self._h, _ptr(act), act.stride(0), _ptr(x), x.stride(0), m, b, e, wp, wb,
                                          _stream(stream, x.device)))
         return act
 

@@ -179,6 +179,25 @@ def test_gate_up_and_down_halves(oracle, hm, device, dtype):
     assert_close(oracle, host_f64(y), host_f64(act) @ wf[2][1024:3072], dtype, "down half")
 
 
+@pytest.mark.parametrize("dtype,group", [("fp16", 128), ("bf16", 64), ("fp16", 32)])
+@pytest.mark.parametrize("m", [7, 16])
+def test_gate_up_split_k_swiglu_combine(oracle, hm, device, dtype, group, m):
+    # hidden 5120 (40 K tiles) at M = 7 (2 splits) or 16 (3 ragged splits) exceeds one staged activation chunk,
+    # so the fused gate_up splits K, writes fp32 gate/up partials and applies SiLU(gate) * up when adding them;
+    # inter 1152 = 72 strip pairs.
+    layer, _, wf = _layer(oracle, hm, device, 5120, 1152, group, dtype, 5)
+    assert layer.workspace_bytes(m) > m * 1152 * 2
+    rng = np.random.default_rng(85 + m)
+    x64, x = make_x(oracle, rng, m, 5120, dtype, device)
+    act = layer.gate_up(x)
+    torch.cuda.synchronize()
+    wg, wu, _ = wf
+    assert_close(oracle, host_f64(act), oracle.silu(x64 @ wg) * (x64 @ wu), dtype, f"split-K gate_up M={m} g={group}")
+    y = layer.forward(x)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, dtype), dtype, f"split-K FFN M={m} g={group}")
+
+
 @pytest.mark.parametrize("layout", ["blocked", "interleaved"])
 @pytest.mark.parametrize("m", [1, 37, 2048])
 def test_silu_mul(oracle, hm, device, layout, m):

@@ -59,6 +59,21 @@ def test_linear_prefix_and_start_column(oracle, hm, device, m):
         assert_close(oracle, host_f64(y), x64 @ wf[:k, col:col + n], dtype, f"prefix k={k} n={n} col={col} M={m}")
 
 
+@pytest.mark.parametrize("group", [64, 128])
+@pytest.mark.parametrize("m", [2, 16])
+def test_linear_odd_strip_count(oracle, hm, device, group, m):
+    # 5 strips of 16 columns: M > 1 cannot pair strips per wave, so one strip per wave; 3 K tiles leave
+    # waves without tiles.
+    rng = np.random.default_rng(600 + group + m)
+    k, n, dtype = 384, 80, "bf16"
+    w_np, w = _matrix(oracle, hm, rng, k, n, group, dtype, device)
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, group, dtype), dtype, f"odd strips g={group} M={m}")
+
+
 def test_linear_split_k_path(oracle, hm, device):
     # M = 16 with K = 14336 does not fit the activation stage in LDS: the GEMV splits K and sums partials.
     rng = np.random.default_rng(400)
