@@ -106,46 +106,76 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     for (int s = 0; s < S; ++s) {
         const int64_t tile0 = static_cast<int64_t>(strip0 + s) * a.kt_pitch + kt0;
         qp[s] = a.quant + tile0 * 64;
-        mp[s] = a.meta + (tile0 * 16 + col) * GPT;
+        mp[s] = a.meta + tile0 * 16 * GPT;
     }
     const int tpw = (nkt + a.wps - 1) / a.wps;
     const int tb = wi * tpw;
     const int te = min(tb + tpw, nkt);
     const int last = te - 1; // >= 0: a wave past the split's end gets te = nkt >= 1 and reads only zero-weighted tiles
 
+    // Activation staging. With one row each wave stages the K range of its own tiles, so no workgroup
+    // barrier stands between the weight stream and the multiply (waves of other strip groups with the same
+    // range write the same values). With several rows the workgroup stages the whole chunk once for its nu
+    // strip groups. Chunks are 8 consecutive K of one row; consecutive lanes take consecutive chunks, so one
+    // group's chunks are G / 8 consecutive lanes.
+    const int chunks_row = kc / 8;
+    const int st_lo = MT == 1 ? tb * 16 : 0;
+    const int st_hi = MT == 1 ? max(te, tb) * 16 : m * chunks_row;
+    const int st_step = MT == 1 ? 64 : WGS;
+    const int st_id = MT == 1 ? lane : tid;
     // Memory requests go out in this order: the activation chunks this thread stages (held in registers),
     // then the first KB steps of the wave's ring. Staging waits for the activations only.
-    const int chunks_row = kc / 8;
-    const int total = m * chunks_row;
     uint4 xv[kPre];
-    auto fetch = [&](int base) { // branch-free: chunks past the end re-read the last one and are not staged
+    auto fetch = [&](int base) { // branch-free: chunks past the end re-read a valid one and are not staged
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            const int idx = min(base + c * WGS + tid, total - 1);
+            const int idx = st_hi > st_lo ? min(st_lo + base + c * st_step + st_id, st_hi - 1) : 0;
             const int row = idx / chunks_row;
             xv[c] = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
         }
     };
     fetch(0);
 
+    // Scale/zero records travel in blocks of RB consecutive tiles: lane l loads the records of tile
+    // i + l / 16 (column l % 16), so one coalesced load covers RB tiles (the records of consecutive tiles
+    // are contiguous), and step u takes its column's record from lane 16 (u % RB) + col.
+    constexpr int RB = KB < 4 ? KB : 4;
+    const int rsub = min(lane >> 4, RB - 1);
     uint4 wq[KB][S];
-    uint32_t rq[KB][S][GPT];
-    // Step u of the ring <- local tile i (already clamped to [0, last]): records first, then the weights.
-    auto load = [&](int u, int i) {
+    // Record blocks of the round being multiplied (rv) and of the next round (rn): a round's steps read rv
+    // while the next round's block is already in flight.
+    uint32_t rv[KB / RB][S][GPT], rn[KB / RB][S][GPT];
+    auto advance = [&]() {
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            if constexpr (GPT == 1) {
-                rq[u][s][0] = mp[s][i * 16];
-            } else if constexpr (GPT == 2) {
-                const uint2 r = *reinterpret_cast<const uint2 *>(mp[s] + i * 32);
-                rq[u][s][0] = r.x;
-                rq[u][s][1] = r.y;
-            } else {
-                const uint4 r = *reinterpret_cast<const uint4 *>(mp[s] + i * 64);
-                rq[u][s][0] = r.x;
-                rq[u][s][1] = r.y;
-                rq[u][s][2] = r.z;
-                rq[u][s][3] = r.w;
+        for (int b = 0; b < KB / RB; ++b) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+#pragma unroll
+                for (int g = 0; g < GPT; ++g) {
+                    rv[b][s][g] = rn[b][s][g];
+                }
+            }
+        }
+    };
+    // Step u of the ring <- local tile i (already clamped to [0, last]): records (every RB steps), then the weights.
+    auto load = [&](int u, int i) {
+        if (u % RB == 0) {
+            const int64_t ri = static_cast<int64_t>(min(i + rsub, last)) * 16 + col;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                if constexpr (GPT == 1) {
+                    rn[u / RB][s][0] = mp[s][ri];
+                } else if constexpr (GPT == 2) {
+                    const uint2 r = *reinterpret_cast<const uint2 *>(mp[s] + ri * 2);
+                    rn[u / RB][s][0] = r.x;
+                    rn[u / RB][s][1] = r.y;
+                } else {
+                    const uint4 r = *reinterpret_cast<const uint4 *>(mp[s] + ri * 4);
+                    rn[u / RB][s][0] = r.x;
+                    rn[u / RB][s][1] = r.y;
+                    rn[u / RB][s][2] = r.z;
+                    rn[u / RB][s][3] = r.w;
+                }
             }
         }
 #pragma unroll
@@ -159,6 +189,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         load(u, min(tb + u, last));
     }
     __builtin_amdgcn_sched_barrier(0);
+    advance();
 
     // 1. Stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes take
     //    consecutive 8-element chunks of a row, so one group is G / 8 consecutive lanes.
@@ -198,18 +229,23 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     };
 #pragma unroll
     for (int c = 0; c < kPre; ++c) {
-        const int idx = c * WGS + tid;
-        stage(idx, xv[c], idx < total); // all lanes take part in the shuffles
+        const int idx = st_lo + c * st_step + st_id;
+        stage(idx, xv[c], idx < st_hi); // all lanes take part in the shuffles
     }
-    for (int base = kPre * WGS; base < total; base += kPre * WGS) {
-        fetch(base); // large M only: these chunks wait behind the first ring steps
+    for (int base = kPre * st_step; st_lo + base < st_hi; base += kPre * st_step) {
+        fetch(base); // long ranges only: these chunks wait behind the first ring steps
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            const int idx = base + c * WGS + tid;
-            stage(idx, xv[c], idx < total);
+            const int idx = st_lo + base + c * st_step + st_id;
+            stage(idx, xv[c], idx < st_hi);
         }
     }
-    lds_barrier(); // not __syncthreads(): its fence would wait for the ring's loads too
+    if constexpr (MT == 1) {
+        // The wave reads only what it wrote; LDS operations of one wave complete in order.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else {
+        lds_barrier(); // not __syncthreads(): its fence would wait for the ring's loads too
+    }
 
     // 2. Multiply. A-operand row of this lane: rows >= m read row m - 1 instead; they only feed D rows >= m,
     //    which are never stored.
@@ -231,7 +267,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     // One step: the S tiles of local tile i (unclamped: tiles past the wave's run are weighted by zero).
     auto step = [&](int u, int i) {
         const int ic = min(i, last);
-        const float live = i < te ? 1.0f : 0.0f;
+        // Tiles past the wave's run are dropped by a select, not a zero weight: a wave without tiles reads
+        // LDS that no wave of its range staged, and NaN * 0 would survive.
+        const bool live = i < te;
         float4_t p[S];
 #pragma unroll
         for (int mu = 0; mu < 4; ++mu) {
@@ -254,13 +292,14 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
                 }
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
-                    const uint32_t rr = rq[u][s][g];
-                    const float sc = T::to_float(rr & 0xFFFFu) * live;
+                    const uint32_t rr = static_cast<uint32_t>(__shfl(static_cast<int>(rv[u / RB][s][g]), 16 * (u % RB) + col));
+                    const float sc = T::to_float(rr & 0xFFFFu);
                     const float z = static_cast<float>((rr >> 16) & 0xFFu);
 #pragma unroll
                     for (int e = 0; e < ROWS; ++e) {
                         const float t = __builtin_fmaf(-z, xsum[e].y, p[s][e] - xsum[e].x);
-                        acc[s][e] = __builtin_fmaf(sc, t, acc[s][e]);
+                        const float upd = __builtin_fmaf(sc, t, acc[s][e]);
+                        acc[s][e] = live ? upd : acc[s][e];
                     }
                 }
             }
@@ -276,6 +315,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             step(u, i);
             load(u, min(i + KB, last));
         }
+        advance();
     }
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
@@ -429,9 +469,11 @@ GemvPlan plan_gemv(const GemvCall &c) {
     const int64_t splits0 = (c.kt_count + max_tiles - 1) / max_tiles;
     p.kt_per_split = (c.kt_count + splits0 - 1) / splits0;
     p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
-    // Waves per strip group: up to 8, keeping at least 8 tiles per wave.
+    // Waves per strip group: up to 8, keeping at least 8 K tiles per wave (16 with a strip pair at M = 1:
+    // measured on the Llama-3-8B gate_up, 32-tile wave runs in 448 workgroups beat 16-tile runs in 896).
+    const int64_t min_run = c.m == 1 ? 8 * p.spw : 8;
     p.wps = 1;
-    while (p.wps < 8 && p.kt_per_split >= 16 * p.wps) {
+    while (p.wps < 8 && p.kt_per_split >= 2 * min_run * p.wps) {
         p.wps *= 2;
     }
     // Strip groups per workgroup: at least 4 waves; with several rows, more groups share one staged chunk

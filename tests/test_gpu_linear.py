@@ -74,6 +74,22 @@ def test_linear_odd_strip_count(oracle, hm, device, group, m):
     assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, group, dtype), dtype, f"odd strips g={group} M={m}")
 
 
+@pytest.mark.parametrize("m", [1, 3])
+def test_linear_waves_without_tiles(oracle, hm, device, monkeypatch, m):
+    # Forced launch shape (tuning overrides): 8 waves per strip over 3 K tiles leaves 5 waves with no tile;
+    # their zero-weighted steps must not leak anything (with M = 1 they read LDS no wave staged).
+    monkeypatch.setenv("HM_GEMV_NU", "1")
+    monkeypatch.setenv("HM_GEMV_WPS", "8")
+    rng = np.random.default_rng(700 + m)
+    k, n, dtype = 384, 64, "fp16"
+    w_np, w = _matrix(oracle, hm, rng, k, n, 128, dtype, device)
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=torch.float16, device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, 128, dtype), dtype, f"idle waves M={m}")
+
+
 def test_linear_split_k_path(oracle, hm, device):
     # M = 16 with K = 14336 does not fit the activation stage in LDS: the GEMV splits K and sums partials.
     rng = np.random.default_rng(400)
