@@ -160,13 +160,24 @@ hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, i
     c.kt_begin = kt_begin;
     c.kt_count = kt_count;
     c.fused = fused;
+    const size_t need = hm::plan_gemm(c).partial_bytes;
+    if (need > workspace_bytes) {
+        return fail(HM_WORKSPACE_TOO_SMALL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+    }
+    c.partial = static_cast<float *>(workspace);
     const hipError_t e = hm::launch_gemm(c, stream);
     return e == hipSuccess ? HM_OK : hip_fail(e, "gemm launch");
 }
 
 size_t linear_workspace(const hm::Planes &p, int64_t M, int64_t n, int64_t kt_count, bool fused) {
     if (M > kGemvMaxRows) {
-        return 0;
+        hm::GemmCall c;
+        c.w = p;
+        c.m = M;
+        c.n = n;
+        c.kt_count = kt_count;
+        c.fused = fused;
+        return hm::plan_gemm(c).partial_bytes;
     }
     hm::GemvCall c;
     c.w = p;
@@ -536,10 +547,16 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
         return 0;
     }
     const size_t act = static_cast<size_t>(round_up(max_m * f->inter * 2, 256));
+    // The largest partial buffer of any M up to max_m (GEMV splits for M <= 16, GEMM K splits above,
+    // which only occur while the output tiles do not fill the chip).
     size_t partial = 0;
-    for (int64_t m = 1; m <= std::min<int64_t>(max_m, kGemvMaxRows); ++m) {
-        partial = std::max(partial, linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false));
-        partial = std::max(partial, linear_workspace(f->gate_up.p, m, f->inter, f->hidden / 128, true));
+    for (int64_t m = 1; m <= max_m; ++m) {
+        const size_t d = linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false);
+        const size_t g = linear_workspace(f->gate_up.p, m, f->inter, f->hidden / 128, true);
+        partial = std::max(partial, std::max(d, g));
+        if (m > kGemvMaxRows && d == 0 && g == 0 && m >= 4096) {
+            break; // at this size every tile configuration fills the chip without splits
+        }
     }
     return act + partial;
 }

@@ -532,21 +532,25 @@ hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
     if (e != hipSuccess || p.splits == 1) {
         return e;
     }
-    const int64_t total = c.m * c.n;
+    return launch_sum_splits(c.partial, c.y, c.ldy, c.m, a.ncols, static_cast<int>(p.splits), c.fused, c.w.dtype, stream);
+}
+
+hipError_t launch_sum_splits(const float *partial, uint16_t *y, int64_t ldy, int64_t m, int ncols, int splits, bool fused,
+                             int dtype, hipStream_t stream) {
+    const int64_t total = m * (fused ? ncols / 2 : ncols);
     const dim3 blocks(static_cast<unsigned>((total + 255) / 256));
-    const int m = static_cast<int>(c.m);
-    const int splits = static_cast<int>(p.splits);
-    if (c.w.dtype == 1) {
-        if (c.fused) {
-            hipLaunchKernelGGL((sum_splits<F16, true>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+    const int mi = static_cast<int>(m);
+    if (dtype == 1) {
+        if (fused) {
+            hipLaunchKernelGGL((sum_splits<F16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
         } else {
-            hipLaunchKernelGGL((sum_splits<F16, false>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+            hipLaunchKernelGGL((sum_splits<F16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
         }
     } else {
-        if (c.fused) {
-            hipLaunchKernelGGL((sum_splits<BF16, true>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+        if (fused) {
+            hipLaunchKernelGGL((sum_splits<BF16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
         } else {
-            hipLaunchKernelGGL((sum_splits<BF16, false>), blocks, dim3(256), 0, stream, c.partial, c.y, c.ldy, m, a.ncols, splits);
+            hipLaunchKernelGGL((sum_splits<BF16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
         }
     }
     return hipGetLastError();

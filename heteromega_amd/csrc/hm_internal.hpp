@@ -78,8 +78,23 @@ struct GemmCall {
     int64_t n = 0;
     int64_t kt_begin = 0, kt_count = 0;
     bool fused = false;
+    float *partial = nullptr; // split-K partials (GemmPlan::partial_bytes)
 };
+// Tile configuration (2: 256 x 256 tiles of 8 waves, 1: 128 x 128 of 4, 0: 64 x 128 of 2). The GEMM
+// does not split K (splits = 1, no partials); the fields keep the GEMV's plan shape.
+struct GemmPlan {
+    int cfg = 1;
+    int64_t tiles_m = 0, tiles_n = 0;
+    int64_t splits = 1, kt_per_split = 0;
+    size_t partial_bytes = 0;
+};
+GemmPlan plan_gemm(const GemmCall &c);
 hipError_t launch_gemm(const GemmCall &c, hipStream_t stream);
+
+// Adds split-K partials [splits][m][ncols] into y [m, ncols] (or, fused, y [m, ncols / 2] = SiLU(gate) * up
+// with gate and up alternating per 16 columns).
+hipError_t launch_sum_splits(const float *partial, uint16_t *y, int64_t ldy, int64_t m, int ncols, int splits, bool fused,
+                             int dtype, hipStream_t stream);
 
 hipError_t launch_silu_mul(const uint16_t *gate_up, int64_t ld_in, uint16_t *act, int64_t ld_out, int64_t rows, int64_t n,
                            bool interleaved, int dtype, hipStream_t stream);
