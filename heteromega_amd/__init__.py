@@ -2,7 +2,7 @@
 
 The compute path is libhmw4a16.so (hand-written HIP kernels behind the C ABI in include/hm_w4a16.h); this
 package is its Python host mirror for tests and harnesses. Importing it loads the library and raises
-ImportError when it has not been built (python -m heteromega_amd.build).
+ImportError when it has not been built (python heteromega_amd/build.py).
 """
 
 from . import _lib

@@ -1,6 +1,6 @@
 """ctypes binding of libhmw4a16.so (include/hm_w4a16.h).
 
-The library is built in-tree by heteromega_amd.build. Loading fails loudly when it is missing: there is no
+The library is built in-tree by heteromega_amd/build.py. Loading fails loudly when it is missing: there is no
 CPU fallback for any compute entry point.
 """
 
@@ -86,7 +86,7 @@ def load():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
-            raise ImportError(f"{LIB_PATH} is missing: run `python -m heteromega_amd.build` (or __graft_entry__.build()) first")
+            raise ImportError(f"{LIB_PATH} is missing: run `python heteromega_amd/build.py` (or __graft_entry__.build()) first")
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in _SIGNATURES.items():
             fn = getattr(L, name)

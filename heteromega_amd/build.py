@@ -1,6 +1,6 @@
 """Builds libhmw4a16.so (the gfx950 kernels and the C ABI of include/hm_w4a16.h) in-tree with hipcc.
 
-Usage: python -m heteromega_amd.build [--verbose]
+Usage: python heteromega_amd/build.py [--verbose]
 """
 
 import os
