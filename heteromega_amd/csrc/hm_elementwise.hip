@@ -59,18 +59,64 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
     if ((threadIdx.x & 63) == 0) {
         scratch[wave] = v;
     }
-    __syncthreads();
+    lds_barrier(); // LDS only: the block's global stores need not complete here
     float t = 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         t += scratch[w];
     }
-    __syncthreads();
+    lds_barrier();
     return t;
 }
 
 // One row per block. ADD: x += y first (stored rounded), and the norm reads the rounded x, as the model's
 // x.add_ then RMSNorm does (src/unified_llm_w4a16_hetero/unified_llm_w4a16.cpp:2815-2821, :2892).
+// Rows of up to kCached * 2048 columns stay in registers: x, y and the weight are requested in one round
+// trip and x is not read back after its residual update.
+constexpr int kCached = 4;
+
+template <class T, bool ADD>
+__device__ __forceinline__ void rmsnorm_cached(uint16_t *__restrict__ out, uint16_t *__restrict__ xr, const uint16_t *__restrict__ yr,
+                                               const uint16_t *__restrict__ w, int64_t cols, float eps, float *scratch) {
+    float v[kCached][8], g[kCached][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kCached; ++j) {
+        const int64_t c = threadIdx.x * 8 + j * 2048;
+        if (c < cols) {
+            load8<T>(xr + c, v[j]);
+            load8<T>(w + c, g[j]);
+            if constexpr (ADD) {
+                float a[8];
+                load8<T>(yr + c, a);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    v[j][k] = T::to_float(T::from_float(v[j][k] + a[k]));
+                }
+                store8<T>(xr + c, v[j]);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                ss += v[j][k] * v[j][k];
+            }
+        }
+    }
+    const float total = block_sum(ss, scratch);
+    const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
+#pragma unroll
+    for (int j = 0; j < kCached; ++j) {
+        const int64_t c = threadIdx.x * 8 + j * 2048;
+        if (c < cols) {
+            float o[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                o[k] = v[j][k] * scale * g[j][k];
+            }
+            store8<T>(out + c, o);
+        }
+    }
+}
+
 template <class T, bool ADD>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(uint16_t *__restrict__ out, int64_t ld_out, uint16_t *__restrict__ x, int64_t ldx,
                                                       const uint16_t *__restrict__ y, int64_t ldy, const uint16_t *__restrict__ w,
@@ -78,6 +124,10 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(uint16_t *__restrict__ out
     __shared__ float scratch[4];
     const int64_t r = blockIdx.x;
     uint16_t *xr = x + r * ldx;
+    if (cols <= kCached * 2048) {
+        rmsnorm_cached<T, ADD>(out + r * ld_out, xr, ADD ? y + r * ldy : nullptr, w, cols, eps, scratch);
+        return;
+    }
     float ss = 0.0f;
     for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
         float v[8];
