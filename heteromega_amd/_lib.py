@@ -53,6 +53,8 @@ _SIGNATURES = {
     "hm_packed_tile_index": (I64, [I64, I64, I64, I64]),
     "hm_pack_w4a16": (ctypes.c_int, [P, P, P, I64, I64, P]),
     "hm_awq_unpack": (ctypes.c_int, [P, I64, I64, P]),
+    "hm_gptq_unpack": (ctypes.c_int, [P, I64, I64, P]),
+    "hm_gptq_unpack_zeros": (ctypes.c_int, [P, I64, I64, I32, P]),
     "hm_weights_from_tiles": (ctypes.c_int, [P, I64, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_weights_from_logical": (ctypes.c_int, [P, P, P, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_weights_to_logical": (ctypes.c_int, [P, P, P, P, P]),
@@ -63,6 +65,7 @@ _SIGNATURES = {
     "hm_linear_workspace_bytes": (SZ, [P, I64, I64, I64]),
     "hm_linear": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I64, I64, P, SZ, P]),
     "hm_ffn_from_tiles": (ctypes.c_int, [P, P, P, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
+    "hm_ffn_from_tiles_padded": (ctypes.c_int, [P, P, P, I64, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_ffn_from_logical": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_ffn_info": (ctypes.c_int, [P, ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(I32)]),
     "hm_ffn_destroy": (ctypes.c_int, [P]),

@@ -288,6 +288,36 @@ hm_status hm_awq_unpack(const int32_t *packed, int64_t rows, int64_t cols8, uint
     return HM_OK;
 }
 
+hm_status hm_gptq_unpack(const int32_t *packed, int64_t rows8, int64_t cols, uint8_t *out) {
+    if (packed == nullptr || out == nullptr || rows8 <= 0 || cols <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_gptq_unpack: bad arguments");
+    }
+    for (int64_t r = 0; r < rows8; ++r) {
+        for (int64_t c = 0; c < cols; ++c) {
+            const uint32_t v = static_cast<uint32_t>(packed[r * cols + c]);
+            for (int k = 0; k < 8; ++k) {
+                out[(8 * r + k) * cols + c] = static_cast<uint8_t>((v >> (4 * k)) & 0xFu);
+            }
+        }
+    }
+    return HM_OK;
+}
+
+hm_status hm_gptq_unpack_zeros(const int32_t *packed, int64_t groups, int64_t cols8, int32_t add_one, uint8_t *out) {
+    if (packed == nullptr || out == nullptr || groups <= 0 || cols8 <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_gptq_unpack_zeros: bad arguments");
+    }
+    for (int64_t g = 0; g < groups; ++g) {
+        for (int64_t j = 0; j < cols8; ++j) {
+            const uint32_t v = static_cast<uint32_t>(packed[g * cols8 + j]);
+            for (int k = 0; k < 8; ++k) {
+                out[g * cols8 * 8 + 8 * j + k] = static_cast<uint8_t>(((v >> (4 * k)) & 0xFu) + (add_one ? 1 : 0));
+            }
+        }
+    }
+    return HM_OK;
+}
+
 hm_status hm_weights_from_tiles(const uint8_t *tiles, int64_t packed_k, int64_t packed_n, int64_t K, int64_t N, hm_dtype dtype,
                                 void *stream, hm_weights **out) {
     if (out == nullptr) {
@@ -414,6 +444,11 @@ hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, in
 
 hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden, int64_t inter, hm_dtype dtype,
                             void *stream, hm_ffn **out) {
+    return hm_ffn_from_tiles_padded(gate, up, down, hidden, inter, hidden, inter, dtype, stream, out);
+}
+
+hm_status hm_ffn_from_tiles_padded(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden, int64_t inter,
+                                   int64_t packed_hidden, int64_t packed_inter, hm_dtype dtype, void *stream, hm_ffn **out) {
     if (out == nullptr) {
         return fail(HM_INVALID_ARGUMENT, "hm_ffn_from_tiles: null output handle");
     }
@@ -426,9 +461,9 @@ hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_
         return fail(HM_INVALID_ARGUMENT, "hm_ffn_from_tiles: hidden and inter must be positive multiples of 128, got %lld, %lld",
                     static_cast<long long>(hidden), static_cast<long long>(inter));
     }
-    if ((st = check_tile_source(gate, hidden, inter, hidden, inter, "gate")) != HM_OK ||
-        (st = check_tile_source(up, hidden, inter, hidden, inter, "up")) != HM_OK ||
-        (st = check_tile_source(down, inter, hidden, inter, hidden, "down")) != HM_OK) {
+    if ((st = check_tile_source(gate, packed_hidden, packed_inter, hidden, inter, "gate")) != HM_OK ||
+        (st = check_tile_source(up, packed_hidden, packed_inter, hidden, inter, "up")) != HM_OK ||
+        (st = check_tile_source(down, packed_inter, packed_hidden, inter, hidden, "down")) != HM_OK) {
         return st;
     }
     auto *f = new hm_ffn;
@@ -446,12 +481,12 @@ hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_
     hm::TileSource gu[2];
     gu[0].tiles = gate;
     gu[1].tiles = up;
-    gu[0].tiles_k = gu[1].tiles_k = hidden / 128;
-    gu[0].tiles_n = gu[1].tiles_n = inter / 64;
+    gu[0].tiles_k = gu[1].tiles_k = packed_hidden / 128;
+    gu[0].tiles_n = gu[1].tiles_n = packed_inter / 64;
     hm::TileSource d;
     d.tiles = down;
-    d.tiles_k = inter / 128;
-    d.tiles_n = hidden / 64;
+    d.tiles_k = packed_inter / 128;
+    d.tiles_n = packed_hidden / 64;
     hipError_t e = hm::launch_repack_tiles(gu, 2, true, const_cast<uint8_t *>(f->gate_up.p.quant), const_cast<uint32_t *>(f->gate_up.p.meta),
                                            hidden, 2 * inter, dtype, as_stream(stream));
     if (e == hipSuccess) {

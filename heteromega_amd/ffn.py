@@ -117,6 +117,31 @@ def awq_unpack_qzeros(qzeros):
     return _awq(qzeros)
 
 
+def gptq_unpack_qweight(qweight):
+    """GPTQ qweight [In/8, Out] int32 -> [In, Out] uint8: nibble i of word (r, o) is row 8r + i
+    (_unpack_gptq_qweight then _unpack_packed_out_in2_to_in_out, llama3_8b_w4a16_model.py:361-378, :398-407)."""
+    p = _host_array(qweight, np.int32)
+    if p.ndim != 2:
+        raise ValueError("gptq_unpack_qweight: qweight must be [In/8, Out]")
+    rows8, cols = p.shape
+    out = np.empty((rows8 * 8, cols), np.uint8)
+    _call(_lib.load().hm_gptq_unpack(p.ctypes.data_as(ctypes.c_void_p), rows8, cols, out.ctypes.data_as(ctypes.c_void_p)))
+    return out
+
+
+def gptq_unpack_qzeros(qzeros, add_one=True):
+    """GPTQ qzeros [G, Out/8] int32 -> [G, Out] uint8, plus one when add_one (1..16; _unpack_gptq_qzeros,
+    llama3_8b_w4a16_model.py:381-395, which returns the transpose [Out, G])."""
+    p = _host_array(qzeros, np.int32)
+    if p.ndim != 2:
+        raise ValueError("gptq_unpack_qzeros: qzeros must be [G, Out/8]")
+    groups, cols8 = p.shape
+    out = np.empty((groups, cols8 * 8), np.uint8)
+    _call(_lib.load().hm_gptq_unpack_zeros(p.ctypes.data_as(ctypes.c_void_p), groups, cols8, 1 if add_one else 0,
+                                           out.ctypes.data_as(ctypes.c_void_p)))
+    return out
+
+
 # ---- repacked matrices ------------------------------------------------------------------------------
 
 class RepackedMatrix:
@@ -280,14 +305,20 @@ class FfnLayer:
         self._ws = {}
 
     @classmethod
-    def from_tiles(cls, gate, up, down, hidden, inter, dtype=torch.bfloat16, stream=None):
-        """From reference-packed device matrices gate [H, I], up [H, I], down [I, H] (GpuFfnModel::add_layer)."""
-        for t in (gate, up, down):
+    def from_tiles(cls, gate, up, down, hidden, inter, dtype=torch.bfloat16, stream=None, packed_hidden=None, packed_inter=None):
+        """From reference-packed device matrices gate [H, I], up [H, I], down [I, H] (GpuFfnModel::add_layer).
+        packed_hidden / packed_inter: the packed extents when the matrices were padded (padPackedWeights,
+        llama3_8b_w4a16_model.py:546-608); the layer is their leading [hidden, inter] block."""
+        ph = hidden if packed_hidden is None else packed_hidden
+        pi = inter if packed_inter is None else packed_inter
+        for t, (k, n) in ((gate, (ph, pi)), (up, (ph, pi)), (down, (pi, ph))):
             if not t.is_cuda or t.dtype != torch.uint8 or not t.is_contiguous():
                 raise ValueError("from_tiles: packed matrices must be contiguous device uint8 tensors")
+            if packed_bytes(k, n) < 0 or t.numel() != packed_bytes(k, n):
+                raise ValueError(f"from_tiles: a packed [{k}, {n}] matrix has {packed_bytes(k, n)} bytes, got {t.numel()}")
         h = ctypes.c_void_p()
-        _call(_lib.load().hm_ffn_from_tiles(_ptr(gate), _ptr(up), _ptr(down), hidden, inter, _hm_dtype(dtype),
-                                            _stream(stream, gate.device), ctypes.byref(h)))
+        _call(_lib.load().hm_ffn_from_tiles_padded(_ptr(gate), _ptr(up), _ptr(down), hidden, inter, ph, pi, _hm_dtype(dtype),
+                                                   _stream(stream, gate.device), ctypes.byref(h)))
         return cls(h, gate.device)
 
     @classmethod
@@ -451,7 +482,12 @@ class GpuFfnModel:
             self.s_prefill = self.s_decode = inter
 
     def add_layer_logical(self, gate, up, down, group, stream=None):
-        layer = FfnLayer.from_logical(gate, up, down, group, self.dtype, stream)
+        self.append(FfnLayer.from_logical(gate, up, down, group, self.dtype, stream))
+
+    def append(self, layer):
+        """Adds a built FfnLayer (of this model's dtype and shape)."""
+        if layer.dtype != self.dtype:
+            raise ValueError(f"GpuFfnModel.append: layer dtype {layer.dtype} differs from the model's {self.dtype}")
         if self._layers and (self._layers[0].hidden != layer.hidden or self._layers[0].inter != layer.inter):
             raise ValueError("GpuFfnModel.add_layer: all layers must have the same shape")
         self._layers.append(layer)
@@ -484,6 +520,6 @@ class GpuFfnModel:
 
 __all__ = [
     "HMError", "kTileK", "kTileN", "kTileBytes", "padded_rows", "packed_bytes", "packed_tile_index", "pack_w4a16",
-    "awq_unpack_qweight", "awq_unpack_qzeros", "RepackedMatrix", "packed_linear", "gemv_w4a16", "gemm_w4a16", "silu_mul",
+    "awq_unpack_qweight", "awq_unpack_qzeros", "gptq_unpack_qweight", "gptq_unpack_qzeros", "RepackedMatrix", "packed_linear", "gemv_w4a16", "gemm_w4a16", "silu_mul",
     "rmsnorm", "residual_add2", "residual_rmsnorm", "FfnLayer", "FFNPartition", "ffn_partitioned", "ffn_row_split", "GpuFfnModel",
 ]

@@ -82,6 +82,19 @@ hm_status hm_pack_w4a16(const uint8_t *q, const uint16_t *scales, const int8_t *
  * (py/unified_llm_w4a16/llama3_8b_w4a16_model.py:325-358). */
 hm_status hm_awq_unpack(const int32_t *packed, int64_t rows, int64_t cols8, uint8_t *out);
 
+/* GPTQ qweight [rows8, cols] int32 -> out [8 * rows8, cols] uint8: nibble k of
+ * word (r, c) is row 8 r + k, column c (sequential order along the input
+ * dimension). Restates _unpack_gptq_qweight + _unpack_packed_out_in2_to_in_out
+ * (py/unified_llm_w4a16/llama3_8b_w4a16_model.py:361-378, :398-407). Host memory. */
+hm_status hm_gptq_unpack(const int32_t *packed, int64_t rows8, int64_t cols, uint8_t *out);
+
+/* GPTQ qzeros [groups, cols8] int32 -> out [groups, 8 * cols8] uint8: nibble k
+ * of word (g, j) is column 8 j + k; add_one adds the 1 that GPTQ checkpoints
+ * subtract when storing (zeros then range 1..16; the engine keeps the zero as a
+ * byte). Restates _unpack_gptq_qzeros (llama3_8b_w4a16_model.py:381-395)
+ * without its transpose (the engine's zeros are [K / group, N]). Host memory. */
+hm_status hm_gptq_unpack_zeros(const int32_t *packed, int64_t groups, int64_t cols8, int32_t add_one, uint8_t *out);
+
 /* ---------------------------------------------------------------------------
  * Repacked weights on the device (CDNA4 strip layout). Created once at load
  * time; the forward entry points read only this layout.
@@ -145,6 +158,14 @@ typedef struct hm_ffn hm_ffn;
  * (replaces GpuFfnModel::add_layer, kernels/gpu/src/gpu_ffn.cpp:122-130). */
 hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden,
                             int64_t inter, hm_dtype dtype, void *stream, hm_ffn **out);
+
+/* Same from matrices stored padded: gate / up packed as [packed_hidden,
+ * packed_inter], down as [packed_inter, packed_hidden] (the reference's
+ * padPackedWeights rounds both up to multiples of 2048 with zeros,
+ * llama3_8b_w4a16_model.py:546-608); the layer is their leading block. */
+hm_status hm_ffn_from_tiles_padded(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden,
+                                   int64_t inter, int64_t packed_hidden, int64_t packed_inter, hm_dtype dtype,
+                                   void *stream, hm_ffn **out);
 
 /* From logical device tensors (see hm_weights_from_logical), any group in {32, 64, 128}:
  * gate/up q [H, I], s/z [H/group, I]; down q [I, H], s/z [I/group, H]. */

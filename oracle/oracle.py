@@ -217,6 +217,25 @@ def awq_unpack(packed):
     return out
 
 
+def gptq_unpack(qweight):
+    """GPTQ qweight [In/8, Out] int32 -> [In, Out] u8: nibble i (bits 4i..4i+3) of word (r, o) is row 8r + i
+    (_unpack_gptq_qweight then _unpack_packed_out_in2_to_in_out, llama3_8b_w4a16_model.py:361-378, :398-407,
+    which go through an [Out, In/2] byte packing and back; the composition is this direct map)."""
+    w = np.ascontiguousarray(qweight, np.int32).view(np.uint32)
+    rows8, cols = w.shape
+    parts = np.stack([(w >> (4 * i)) & 0xF for i in range(8)], axis=1)  # [In/8, 8, Out]
+    return parts.reshape(rows8 * 8, cols).astype(np.uint8)
+
+
+def gptq_unpack_zeros(qzeros, add_one=True):
+    """GPTQ qzeros [G, Out/8] int32 -> [G, Out] u8, nibble i of word (g, j) is column 8j + i, plus one when add_one
+    (_unpack_gptq_qzeros, llama3_8b_w4a16_model.py:381-395, without its final transpose)."""
+    w = np.ascontiguousarray(qzeros, np.int32).view(np.uint32)
+    g, cols8 = w.shape
+    parts = np.stack([(w >> (4 * i)) & 0xF for i in range(8)], axis=2)  # [G, Out/8, 8]
+    return (parts.reshape(g, cols8 * 8) + (1 if add_one else 0)).astype(np.uint8)
+
+
 # ---- float reference ---------------------------------------------------------------------------------
 
 def silu(v):
