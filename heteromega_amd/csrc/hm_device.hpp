@@ -135,6 +135,8 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // Wave-uniform value as a scalar (lets the compiler keep wave indices and tile loops in SGPRs).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// SiLU with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division: the result is rounded to
+// fp16 / bf16 next, far coarser than the reciprocal's error. g -> -inf gives -0, g -> +inf gives g.
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 } // namespace hm

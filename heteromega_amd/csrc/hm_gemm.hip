@@ -2,24 +2,30 @@
 //
 // The B operand of v_mfma_f32_16x16x32 (lane l: column l % 16, K 8 (l / 16) .. + 7 of a 32-K step) is the
 // strip layout itself (hm_device.hpp): one 16-byte load per lane brings a strip tile's four 32-K steps. So
-// each wave loads the nibbles of its own 4 strips straight from memory into registers (no LDS, and no other
+// each wave loads the nibbles of its own strips straight from memory into registers (no LDS, and no other
 // wave dequantizes the same columns), turns each step's dword into (q - z) * s in the activation type, and
 // multiplies it with activation fragments read from LDS. The weight rounding to fp16 / bf16 happens once per
 // weight, as in the reference GEMM (src/hipkernels/w4a16_gemm_packed.cu:491-497); accumulation is fp32.
 //
-// Workgroup = WM x WN waves over a BM x BN output tile, BM = WM * RBW * 16 rows, BN = WN * 64 columns; a wave
-// owns RBW row blocks of 16 x its 4 strips. The activation tile (BM x 128 per K tile) is double-buffered in
-// LDS: the next K tile's activation chunks and strip tiles are requested before the current one is
-// multiplied, written to the other buffer after it, and one barrier per K tile separates the two.
+// Workgroup = 4 waves side by side over a BM x 128 output tile; a wave owns all BM = 16 RBW rows of 2 strips
+// (32 columns), so each dequantized B operand feeds RBW MFMAs (8 at BM = 128: about two VALU instructions per
+// MFMA). The activation tile (BM x 128 per K tile) goes from memory straight into LDS (buffer_load ... lds, no
+// registers), double-buffered, its 16-byte chunks XOR-swizzled by row so that an MFMA operand read touches 16
+// distinct bank groups; one barrier per K tile.
+//
+// Software pipeline: while the MFMAs of 32-K step mu run, the VALU builds the B operands of step mu + 1 (of the
+// next K tile at mu = 3) and the LDS delivers the activation fragments of step mu + 1; sched_group_barrier
+// interleaves one MFMA with two VALU instructions. The next K tile's weights and activations are requested at
+// the start of each K tile.
 //
 // Tiles are dealt to XCDs in contiguous runs (workgroup i runs on XCD i % 8), row tile outermost, so the
 // workgroups resident on one XCD share activation rows in its L2 while the weights stream.
 //
 // D element i of lane l is row 4 (l / 16) + i, column l % 16. Fused (gate_up, strips alternating gate / up
-// per 16 channels): a wave's strips 2j and 2j + 1 are the gate and up columns of the same channels in the same
-// lanes, so the epilogue writes SiLU(gate) * up with fp32 math and one rounding
-// (kernels/gpu/src/gemm_w4a16.cu:229-275 fuses the same way). K splits write fp32 partials instead, which the
-// split reduction adds (and applies SwiGLU to when fused).
+// per 16 channels): a wave's two strips are the gate and up columns of the same channels in the same lanes, so
+// the epilogue writes SiLU(gate) * up with fp32 math and one rounding (kernels/gpu/src/gemm_w4a16.cu:229-275
+// fuses the same way). The K range is never split, so every output element accumulates in the same order for
+// any M and tile shape.
 #include "hm_device.hpp"
 #include "hm_internal.hpp"
 
@@ -30,8 +36,6 @@ namespace hm {
 namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kAStride = 128 + 8; // halves per staged activation row (padding spreads LDS banks)
 
 struct GemmArgs {
     const uint4 *quant;
@@ -102,27 +106,41 @@ __device__ __forceinline__ uint4 dequant_operand(uint32_t w, const Deq<BF16> &q,
 }
 
 template <class T, int G, int NSW> struct BTile {
-    u32x4_t w[NSW];                  // strip dwords of one K tile
-    uint32_t r[NSW][128 / G];        // scale/zero records of its groups
+    u32x4_t w[NSW];           // strip dwords of one K tile
+    uint32_t r[NSW][128 / G]; // scale/zero records of its groups
 };
 
-template <class T, int G, bool FUSED, int WM, int WN, int RBW, int NSW, int OCC>
-__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(OCC))) gemm_kernel(GemmArgs a) {
-    constexpr int WGS = WM * WN * 64;
-    constexpr int BM = WM * RBW * 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (buffer_load_dwordx4 ... lds). The host
+// pass of hipcc does not instantiate kernels that name this builtin, so only the device pass sees it.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
+#endif
+}
+
+template <class T, int G, bool FUSED, int RBW, int NSW, int WN>
+__global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2))) gemm_kernel(GemmArgs a) {
+    constexpr int WGS = WN * 64;
+    constexpr int BM = RBW * 16;
     constexpr int BN = WN * NSW * 16;
     constexpr int GPT = 128 / G;
     constexpr int SPG = 4 / GPT;       // 32-K steps per group
-    constexpr int ACH = BM * 16 / WGS; // 16-byte activation chunks per thread per K tile
-    constexpr int AH = ACH / 2;
-    static_assert(AH * 2 == ACH, "activation halves");
-    __shared__ __align__(16) uint16_t as[2][BM * kAStride];
+    constexpr int ADMA = BM * 16 / WGS; // 1 KiB activation transfers per wave per K tile
+    static_assert(ADMA * WGS == BM * 16, "activation transfers");
+    // Activation tile of one K tile: BM rows of 128 halves (256 B), 16-byte chunks XOR-swizzled by row
+    // (chunk c of row r at slot c ^ (r % 16)), so the 16 rows one MFMA operand read touches fall on distinct banks.
+    // Two separate arrays (not one [2][...]) so that the compiler can tell the buffers apart and does not
+    // make reads of one wait for the transfers into the other.
+    __shared__ __align__(1024) uint8_t as0[BM * 256];
+    __shared__ __align__(1024) uint8_t as1[BM * 256];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = uniform(tid >> 6);
-    const int wm = wave / WN;
-    const int wn = wave % WN;
     const int col = lane & 15;
     const int h = lane >> 4;
 
@@ -136,61 +154,61 @@ __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_
     const int row0 = tm * BM;
     const int nkt = a.kt_count;
 
-    // Byte offsets (32-bit) from uniform bases, so loads take the scalar-base + vector-offset form.
-    const uint8_t *qb = reinterpret_cast<const uint8_t *>(a.quant);
-    const uint8_t *mb = reinterpret_cast<const uint8_t *>(a.meta);
-    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x);
-    const int sbase = tn * (BN / 16) + wn * NSW; // strip index within the call
-    const uint32_t tile0 = static_cast<uint32_t>(a.strip_begin + sbase) * a.kt_pitch + a.kt_begin;
-    const uint32_t qoff = tile0 * 1024u + lane * 16u;
-    const uint32_t moff = (tile0 * 16u + col) * GPT * 4u;
+    // Buffer resources with per-wave bases; per K tile only the scalar offset moves.
+    const int sbase = tn * (BN / 16) + wave * NSW; // first strip of this wave within the call
+    const int64_t tile0 = static_cast<int64_t>(a.strip_begin + sbase) * a.kt_pitch + a.kt_begin;
     const uint32_t qstrip = static_cast<uint32_t>(a.kt_pitch) * 1024u;
     const uint32_t mstrip = static_cast<uint32_t>(a.kt_pitch) * 64u * GPT;
-    uint32_t aoff[ACH]; // activation chunk c = tid + WGS j: row c / 16 (rows past M read row M - 1), K 8 (c % 16)
+    const __amdgpu_buffer_rsrc_t qr = buffer_rsrc(reinterpret_cast<const uint8_t *>(a.quant) + tile0 * 1024, NSW * qstrip);
+    const __amdgpu_buffer_rsrc_t mr = buffer_rsrc(reinterpret_cast<const uint8_t *>(a.meta) + tile0 * 64 * GPT, NSW * mstrip);
+    const uint32_t ldx2 = static_cast<uint32_t>(a.ldx) * 2u;
+    const int rows_here = min(BM, a.m - row0);
+    // x column 0 is the call's first K (kt_begin), as for the GEMV.
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(reinterpret_cast<const uint8_t *>(a.x) + static_cast<int64_t>(row0) * a.ldx * 2,
+                                                  static_cast<uint32_t>(rows_here - 1) * ldx2 + static_cast<uint32_t>(nkt) * 256u);
+    // Transfer j of this wave fills LDS bytes [(wave * ADMA + j) KiB, +1 KiB): lane l -> slot p = 64 (wave ADMA + j) + l,
+    // row p / 16, swizzled chunk p % 16 (so source chunk (p % 16) ^ (row % 16)). Rows past M read row M - 1.
+    uint32_t xoff[ADMA];
 #pragma unroll
-    for (int j = 0; j < ACH; ++j) {
-        const int c = tid + WGS * j;
-        const uint32_t gr = static_cast<uint32_t>(min(row0 + (c >> 4), a.m - 1));
-        aoff[j] = (gr * static_cast<uint32_t>(a.ldx) + static_cast<uint32_t>((c & 15) * 8)) * 2u;
+    for (int j = 0; j < ADMA; ++j) {
+        const int p = (wave * ADMA + j) * 64 + lane;
+        const int r = p >> 4;
+        const int c = (p & 15) ^ (r & 15);
+        xoff[j] = static_cast<uint32_t>(min(r, rows_here - 1)) * ldx2 + static_cast<uint32_t>(c) * 16u;
     }
+    const uint32_t qoff = static_cast<uint32_t>(lane) * 16u;
+    const uint32_t moff = static_cast<uint32_t>(col) * GPT * 4u;
 
-    u32x4_t av[AH];
-    auto load_a = [&](int kt, int half) __attribute__((always_inline)) {
-        const uint8_t *xk = xb + static_cast<uint32_t>(kt) * 256u;
-#pragma unroll
-        for (int j = 0; j < AH; ++j) {
-            av[j] = *reinterpret_cast<const u32x4_t *>(xk + aoff[half * AH + j]);
-        }
-    };
-    auto store_a = [&](int buf, int half) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < AH; ++j) {
-            const int c = tid + WGS * (half * AH + j);
-            *reinterpret_cast<u32x4_t *>(as[buf] + (c >> 4) * kAStride + (c & 15) * 8) = av[j];
-        }
-    };
     auto load_b = [&](int kt, BTile<T, G, NSW> &bt) __attribute__((always_inline)) {
-        const uint8_t *mk = mb + static_cast<uint32_t>(kt) * (64u * GPT);
-        const uint8_t *qk = qb + static_cast<uint32_t>(kt) * 1024u;
 #pragma unroll
         for (int s = 0; s < NSW; ++s) {
+            const uint32_t mo = moff + s * mstrip;
+            const uint32_t ms = static_cast<uint32_t>(kt) * (64u * GPT);
             if constexpr (GPT == 1) {
-                bt.r[s][0] = *reinterpret_cast<const uint32_t *>(mk + moff + s * mstrip);
+                bt.r[s][0] = __builtin_amdgcn_raw_buffer_load_b32(mr, mo, ms, 0);
             } else if constexpr (GPT == 2) {
-                const uint2 v = *reinterpret_cast<const uint2 *>(mk + moff + s * mstrip);
-                bt.r[s][0] = v.x;
-                bt.r[s][1] = v.y;
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(mr, mo, ms, 0);
+                bt.r[s][0] = v[0];
+                bt.r[s][1] = v[1];
             } else {
-                const uint4 v = *reinterpret_cast<const uint4 *>(mk + moff + s * mstrip);
-                bt.r[s][0] = v.x;
-                bt.r[s][1] = v.y;
-                bt.r[s][2] = v.z;
-                bt.r[s][3] = v.w;
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(mr, mo, ms, 0);
+                bt.r[s][0] = v[0];
+                bt.r[s][1] = v[1];
+                bt.r[s][2] = v[2];
+                bt.r[s][3] = v[3];
             }
         }
 #pragma unroll
         for (int s = 0; s < NSW; ++s) {
-            bt.w[s] = *reinterpret_cast<const u32x4_t *>(qk + qoff + s * qstrip);
+            bt.w[s] = __builtin_amdgcn_raw_buffer_load_b128(qr, qoff + s * qstrip, static_cast<uint32_t>(kt) * 1024u, 0);
+        }
+    };
+    // Activation chunks of K tile kt straight into LDS buffer buf (no registers).
+    auto load_a = [&](int kt, int buf) __attribute__((always_inline)) {
+        const uint32_t so = static_cast<uint32_t>(kt) * 256u;
+#pragma unroll
+        for (int j = 0; j < ADMA; ++j) {
+            lds_dma16(xr, (buf ? as1 : as0) + (wave * ADMA + j) * 1024, xoff[j], so);
         }
     };
 
@@ -204,61 +222,94 @@ __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_
     }
     const MagicRegs magic = magic_regs<T>();
 
-    // One K tile: multiply `cur` with activation buffer `buf` while K tile `ktn` is requested into `nxt` and
-    // the other buffer.
-    auto iteration = [&](int kt, int buf, const BTile<T, G, NSW> &cur, BTile<T, G, NSW> &nxt) __attribute__((always_inline)) {
-        const int ktn = min(kt + 1, nkt - 1); // the last iteration re-requests its own tile; nothing reads it
-        load_a(ktn, 0);
-        load_b(ktn, nxt);
-        Deq<T> dq[NSW][GPT];
+    // Software pipeline over the 32-K steps: while the MFMAs of step mu run, the VALU builds the B operands of
+    // step mu + 1 (of the next K tile when mu = 3) and the LDS delivers the activation fragments of step mu + 1.
+    struct BOps {
+        uint4 v[NSW];
+    };
+    struct AFr {
+        uint4 v[RBW];
+    };
+    // B operands of step mu of tile bt with the constants dqg of its group; the constants are rebuilt when a group starts.
+    auto dequant_step = [&](const BTile<T, G, NSW> &bt, Deq<T> (&dqg)[NSW], int mu, BOps &o) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < NSW; ++s) {
-#pragma unroll
-            for (int g = 0; g < GPT; ++g) {
-                dq[s][g] = make_deq(cur.r[s][g], T{});
+            if (mu % SPG == 0) {
+                dqg[s] = make_deq(bt.r[s][mu / SPG], T{});
             }
+            o.v[s] = dequant_operand(bt.w[s][mu], dqg[s], magic);
         }
-        const uint16_t *ab = as[buf] + (wm * RBW * 16 + col) * kAStride + 8 * h;
+    };
+    // Fragment of row block rb, step mu: row rb * 16 + col, chunk 4 mu + h at its swizzled slot.
+    const uint32_t aread = static_cast<uint32_t>(col) * 256u;
+    auto read_a = [&](int buf, int mu, AFr &f) __attribute__((always_inline)) {
+        const uint8_t *ab = (buf ? as1 : as0) + aread + (((4 * mu + h) ^ col) << 4);
+#pragma unroll
+        for (int rb = 0; rb < RBW; ++rb) {
+            f.v[rb] = *reinterpret_cast<const uint4 *>(ab + rb * 4096);
+        }
+    };
+
+    // One K tile. On entry `op` holds step 0's B operands of `cur`, `dq` the constants of `cur`, `fa` step 0's
+    // activation fragments; on exit the same for K tile kt + 1.
+    auto iteration = [&](int kt, int buf, const BTile<T, G, NSW> &cur, BTile<T, G, NSW> &nxt, Deq<T> (&dq)[NSW], BOps &op,
+                         AFr &fa) __attribute__((always_inline)) {
+        const int ktn = min(kt + 1, nkt - 1); // the last iteration re-requests its own tile; nothing reads it
+        load_b(ktn, nxt);
+        load_a(ktn, buf ^ 1); // that buffer was last read before the previous barrier
 #pragma unroll
         for (int mu = 0; mu < 4; ++mu) {
-            uint4 bv[NSW];
+            BOps on;
+            AFr fn;
+            if (mu < 3) {
+                read_a(buf, mu + 1, fn);
+                dequant_step(cur, dq, mu + 1, on);
+            } else {
+                wait_vmcnt<ADMA>(); // nxt's weights (the activation transfers behind them may still run)
+                dequant_step(nxt, dq, 0, on);
+            }
+            // strip-major: the operand of the last strip, finished at the end of the previous step, is needed last
 #pragma unroll
             for (int s = 0; s < NSW; ++s) {
-                bv[s] = dequant_operand(cur.w[s][mu], dq[s][mu / SPG], magic);
-            }
 #pragma unroll
-            for (int rb = 0; rb < RBW; ++rb) {
-                const uint4 a4 = *reinterpret_cast<const uint4 *>(ab + rb * 16 * kAStride + 32 * mu);
-#pragma unroll
-                for (int s = 0; s < NSW; ++s) {
-                    acc[rb][s] = T::mfma16(a4, bv[s], acc[rb][s]);
+                for (int rb = 0; rb < RBW; ++rb) {
+                    acc[rb][s] = T::mfma16(fa.v[rb], op.v[s], acc[rb][s]);
                 }
             }
-            if (mu == 1) {
-                store_a(buf ^ 1, 0); // that buffer was last read before the previous barrier
-                load_a(ktn, 1);
+#pragma unroll
+            for (int i = 0; i < RBW * NSW; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0); // then a share of the next step's operand build
             }
-            __builtin_amdgcn_sched_barrier(0); // one 32-K step's fragments live at a time
+            __builtin_amdgcn_sched_barrier(0);
+            op = on;
+            if (mu < 3) {
+                fa = fn;
+            }
         }
-        store_a(buf ^ 1, 1);
-        lds_barrier();
+        // The next tile's activations: this wave's transfers done, then everyone's.
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        read_a(buf ^ 1, 0, fa);
     };
 
     BTile<T, G, NSW> b0, b1;
-    load_a(0, 0);
     load_b(0, b0);
-    store_a(0, 0);
-    load_a(0, 1);
-    store_a(0, 1);
-    lds_barrier();
+    load_a(0, 0);
+    Deq<T> dq[NSW];
+    BOps op;
+    AFr fa;
+    wait_vmcnt<ADMA>();
+    dequant_step(b0, dq, 0, op);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    read_a(0, 0, fa);
     // Two K tiles per trip, so the register sets alternate without copies.
     int kt = 0;
     for (; kt + 1 < nkt; kt += 2) {
-        iteration(kt, 0, b0, b1);
-        iteration(kt + 1, 1, b1, b0);
+        iteration(kt, 0, b0, b1, dq, op, fa);
+        iteration(kt + 1, 1, b1, b0, dq, op, fa);
     }
     if (kt < nkt) {
-        iteration(kt, 0, b0, b1);
+        iteration(kt, 0, b0, b1, dq, op, fa);
     }
 
     // Epilogue.
@@ -266,7 +317,7 @@ __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_
     for (int rb = 0; rb < RBW; ++rb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = row0 + wm * RBW * 16 + rb * 16 + 4 * h + i;
+            const int row = row0 + rb * 16 + 4 * h + i;
             if (row >= a.m) {
                 continue;
             }
@@ -286,24 +337,21 @@ __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_
     }
 }
 
-template <class T, int G, int WM, int WN, int RBW, int NSW, int OCC>
-hipError_t launch_cfg(const GemmArgs &a, bool fused, dim3 grid, hipStream_t s) {
+template <class T, int G, int RBW, int NSW, int WN> hipError_t launch_cfg(const GemmArgs &a, bool fused, dim3 grid, hipStream_t s) {
     if (fused) {
-        hipLaunchKernelGGL((gemm_kernel<T, G, true, WM, WN, RBW, NSW, OCC>), grid, dim3(WM * WN * 64), 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel<T, G, true, RBW, NSW, WN>), grid, dim3(WN * 64), 0, s, a);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<T, G, false, WM, WN, RBW, NSW, OCC>), grid, dim3(WM * WN * 64), 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel<T, G, false, RBW, NSW, WN>), grid, dim3(WN * 64), 0, s, a);
     }
     return hipGetLastError();
 }
 
 template <class T, int G> hipError_t launch_g(const GemmArgs &a, bool fused, int cfg, dim3 grid, hipStream_t s) {
     switch (cfg) {
-    case 2:
-        return launch_cfg<T, G, 2, 2, 8, 4, 1>(a, fused, grid, s); // 256 x 128, 4 waves of 128 x 64
     case 1:
-        return launch_cfg<T, G, 2, 2, 4, 4, 2>(a, fused, grid, s); // 128 x 128, 4 waves of 64 x 64
+        return launch_cfg<T, G, 8, 2, 4>(a, fused, grid, s); // 128 x 128, 4 waves of 128 x 32
     default:
-        return launch_cfg<T, G, 1, 2, 4, 4, 2>(a, fused, grid, s); // 64 x 128, 2 waves of 64 x 64
+        return launch_cfg<T, G, 4, 2, 4>(a, fused, grid, s); // 64 x 128, 4 waves of 64 x 32
     }
 }
 
@@ -325,17 +373,17 @@ constexpr int kCUs = 256;
 GemmPlan plan_gemm(const GemmCall &c) {
     GemmPlan p;
     const int64_t cols = c.fused ? 2 * c.n : c.n;
-    // 128 x 128 tiles (4 waves) when their grid fills the chip, else 64 x 128 (2 waves). The K range is never
-    // split: every output element then accumulates in the same order for any M and tile shape, so a row block
-    // computed alone gives the same bits as inside a larger call.
+    // 128 x 128 tiles when their grid fills the chip, else 64 x 128 (4 waves each). The K range is never split:
+    // every output element then accumulates in the same order for any M and tile shape, so a row block computed
+    // alone gives the same bits as inside a larger call.
     p.cfg = ((c.m + 127) / 128) * (cols / 128) >= kCUs ? 1 : 0;
     if (const char *v = std::getenv("HM_GEMM_CFG")) { // tuning override
         const int cfg = std::atoi(v);
-        if (cfg >= 0 && cfg <= 2) {
+        if (cfg >= 0 && cfg <= 1) {
             p.cfg = cfg;
         }
     }
-    const int64_t bm = p.cfg == 2 ? 256 : p.cfg == 1 ? 128 : 64;
+    const int64_t bm = p.cfg == 1 ? 128 : 64;
     const int64_t bn = 128;
     p.tiles_m = (c.m + bm - 1) / bm;
     p.tiles_n = cols / bn;

@@ -80,8 +80,8 @@ struct GemmCall {
     bool fused = false;
     float *partial = nullptr; // split-K partials (GemmPlan::partial_bytes)
 };
-// Tile configuration (2: 256 x 256 tiles of 8 waves, 1: 128 x 128 of 4, 0: 64 x 128 of 2). The GEMM
-// does not split K (splits = 1, no partials); the fields keep the GEMV's plan shape.
+// Tile configuration (1: 128 x 128 tiles, 0: 64 x 128, 4 waves each). The GEMM does not split K (splits = 1,
+// no partials); the fields keep the GEMV's plan shape.
 struct GemmPlan {
     int cfg = 1;
     int64_t tiles_m = 0, tiles_n = 0;
