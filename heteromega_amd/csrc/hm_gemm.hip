@@ -312,25 +312,26 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
         iteration(kt, 0, b0, b1, dq, op, fa);
     }
 
-    // Epilogue.
+    // Epilogue through a buffer covering this tile's valid rows: stores of rows past M fall outside it and are
+    // dropped by the buffer range check, so no per-row branch; row offsets are scalar.
+    const uint32_t ldy2 = static_cast<uint32_t>(a.ldy) * 2u;
+    const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(a.y + static_cast<int64_t>(row0) * a.ldy, static_cast<uint32_t>(rows_here) * ldy2);
+    const uint32_t ycol = static_cast<uint32_t>(4 * h) * ldy2 + static_cast<uint32_t>(FUSED ? sbase / 2 * 16 + col : sbase * 16 + col) * 2u;
 #pragma unroll
     for (int rb = 0; rb < RBW; ++rb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = row0 + rb * 16 + 4 * h + i;
-            if (row >= a.m) {
-                continue;
-            }
+            const uint32_t ro = static_cast<uint32_t>(rb * 16 + i) * ldy2;
             if constexpr (FUSED) {
 #pragma unroll
                 for (int s = 0; s < NSW; s += 2) {
-                    const int ch = (sbase + s) / 2 * 16 + col;
-                    a.y[static_cast<int64_t>(row) * a.ldy + ch] = T::from_float(silu(acc[rb][s][i]) * acc[rb][s + 1][i]);
+                    const uint16_t v = T::from_float(silu(acc[rb][s][i]) * acc[rb][s + 1][i]);
+                    __builtin_amdgcn_raw_buffer_store_b16(v, yr, ycol + (s / 2) * 32u, ro, 0);
                 }
             } else {
 #pragma unroll
                 for (int s = 0; s < NSW; ++s) {
-                    a.y[static_cast<int64_t>(row) * a.ldy + (sbase + s) * 16 + col] = T::from_float(acc[rb][s][i]);
+                    __builtin_amdgcn_raw_buffer_store_b16(T::from_float(acc[rb][s][i]), yr, ycol + s * 32u, ro, 0);
                 }
             }
         }
