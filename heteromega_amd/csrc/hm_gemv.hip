@@ -57,6 +57,30 @@ struct GemvArgs {
     int wps;   // waves per strip group
 };
 
+// v plus v of another lane of the same row of 16 (DPP control CTRL).
+template <int CTRL> __device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of v over aligned groups of N (1, 2, 4, 8 or 16) consecutive lanes, in every lane of the group, by DPP
+// butterflies within a row of 16 lanes: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+template <int N> __device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group of lanes");
+    if constexpr (N >= 2) {
+        v = dpp_add<0xB1>(v);
+    }
+    if constexpr (N >= 4) {
+        v = dpp_add<0x4E>(v);
+    }
+    if constexpr (N >= 8) {
+        v = dpp_add<0x141>(v);
+    }
+    if constexpr (N >= 16) {
+        v = dpp_add<0x140>(v);
+    }
+    return v;
+}
+
 // Dynamic LDS: xs [m][kc + 8] 16-bit, sums [m][kc / G + 1] float2 (Xb, X); after the multiply the front of
 // the same space holds red [waves][S][m][16] float.
 template <class T, int MT, int G, int S, bool FUSED, int WGS>
@@ -75,7 +99,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int tid = threadIdx.x;
     const int wave = uniform(tid >> 6);
     const int lane = tid & 63;
-    const int m = a.m;
+    const int m = MT == 1 ? 1 : a.m; // the one-row instantiation is launched for m = 1 only
     const int col = lane & 15;
     const int h = lane >> 4;
 
@@ -130,7 +154,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
             const int idx = st_hi > st_lo ? min(st_lo + base + c * st_step + st_id, st_hi - 1) : 0;
-            const int row = idx / chunks_row;
+            const int row = MT == 1 ? 0 : idx / chunks_row;
             xv[c] = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
         }
     };
@@ -197,16 +221,24 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         float sa = 0.0f, sb = 0.0f;
         int row = 0, c8 = 0;
         if (valid) {
-            row = idx / chunks_row;
+            row = MT == 1 ? 0 : idx / chunks_row;
             c8 = idx - row * chunks_row;
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            if constexpr (T::kWide) {
+                // fp16: sums of the even / odd pairs with v_dot2_f32_f16 against (1, 1)
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const h2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+                sa = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.z), one, __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.x), one, 0.0f, false), false);
+                sb = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.w), one, __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.y), one, 0.0f, false), false);
+            } else {
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const float lo = T::to_float(w[p] & 0xFFFFu), hi = T::to_float(w[p] >> 16);
-                if (p & 1) {
-                    sb += lo + hi;
-                } else {
-                    sa += lo + hi;
+                for (int p = 0; p < 4; ++p) {
+                    const float lo = T::to_float(w[p] & 0xFFFFu), hi = T::to_float(w[p] >> 16);
+                    if (p & 1) {
+                        sb += lo + hi;
+                    } else {
+                        sa += lo + hi;
+                    }
                 }
             }
             if constexpr (T::kWide) {
@@ -217,11 +249,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             }
             *reinterpret_cast<uint4 *>(xs + row * xst + c8 * 8) = v;
         }
-#pragma unroll
-        for (int off = 1; off < CPG; off <<= 1) {
-            sa += __shfl_xor(sa, off);
-            sb += __shfl_xor(sb, off);
-        }
+        // Sum over the CPG consecutive lanes of a group with DPP (no LDS crossbar): pairs, quads, eights, sixteens.
+        sa = group_sum<CPG>(sa);
+        sb = group_sum<CPG>(sb);
         if (valid && (c8 % CPG) == 0) {
             const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
             sums[row * sst + c8 / CPG] = make_float2(xb, sa + sb);
