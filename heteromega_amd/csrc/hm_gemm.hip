@@ -55,8 +55,10 @@ struct GemmArgs {
 // Per (strip, group) dequantization constants, made once per K tile from the scale/zero record.
 template <class T> struct Deq;
 // fp16: d2 = (1024 + z) in both halves, s2 = s in both halves.
+// fp16 with the wide nibble positions: pairs 1 and 3 of a dword come out as 1024 + 16 q, so they take
+// d2w = 1024 + 16 z and s2w = s / 16 (exact for s >= 2^-10; smaller scales lose their low bits in s / 16).
 template <> struct Deq<F16> {
-    uint32_t d2, s2;
+    uint32_t d2, s2, d2w, s2w;
 };
 // bf16: s and -(128 + z) s in fp32 (both exact).
 template <> struct Deq<BF16> {
@@ -64,9 +66,13 @@ template <> struct Deq<BF16> {
 };
 
 __device__ __forceinline__ Deq<F16> make_deq(uint32_t rec, F16) {
-    const uint32_t d = 0x6400u | ((rec >> 16) & 0xFFu); // fp16 bits of 1024 + z (z < 16)
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t z = (rec >> 16) & 0xFFu;
+    const uint32_t d = 0x6400u + z;      // fp16 bits of 1024 + z (z <= 16)
+    const uint32_t dw = 0x6400u + 16u * z; // fp16 bits of 1024 + 16 z
     const uint32_t sb = rec & 0xFFFFu;
-    return Deq<F16>{d | (d << 16), sb | (sb << 16)};
+    const h2 s16 = __builtin_bit_cast(h2, sb | (sb << 16)) * h2{static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    return Deq<F16>{d | (d << 16), sb | (sb << 16), dw | (dw << 16), __builtin_bit_cast(uint32_t, s16)};
 }
 
 __device__ __forceinline__ Deq<BF16> make_deq(uint32_t rec, BF16) {
@@ -80,13 +86,15 @@ __device__ __forceinline__ uint4 dequant_operand(uint32_t w, const Deq<F16> &q, 
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const h2 d2 = __builtin_bit_cast(h2, q.d2);
     const h2 s2 = __builtin_bit_cast(h2, q.s2);
+    const h2 d2w = __builtin_bit_cast(h2, q.d2w);
+    const h2 s2w = __builtin_bit_cast(h2, q.s2w);
+    const uint32_t u = w >> 8;
+    // dword i holds K elements 2i, 2i + 1 (nibbles i and 4 + i); (16 (q - z)) (s / 16) = (q - z) s exactly
     uint4 b;
-    uint32_t *o = reinterpret_cast<uint32_t *>(&b);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t v = ((w >> (4 * i)) & m.lo) | m.magic;
-        o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, v) - d2) * s2);
-    }
+    b.x = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, (w & m.lo) | m.magic) - d2) * s2);
+    b.y = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, (w & m.hi) | m.magic) - d2w) * s2w);
+    b.z = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, (u & m.lo) | m.magic) - d2) * s2);
+    b.w = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, (u & m.hi) | m.magic) - d2w) * s2w);
     return b;
 }
 

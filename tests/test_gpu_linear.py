@@ -31,6 +31,22 @@ def test_linear_vs_oracle(oracle, hm, device, dtype, m):
     assert_close(oracle, host_f64(y), ref, dtype, f"linear M={m} [{k}x{n}] g={g}")
 
 
+@pytest.mark.parametrize("m", [1, 16, 200])
+def test_linear_tiny_scales(oracle, hm, device, m):
+    # fp16 scales below 2^-10 (and subnormal ones): the GEMM's odd pairs multiply by s / 16, which then loses
+    # low bits; the result must stay within the tolerance.
+    rng = np.random.default_rng(150 + m)
+    k, n, g = 1024, 512, 128
+    w_np = oracle.random_weights(rng, k, n, g, "fp16", 1e-6, 9e-4)
+    w = hm.RepackedMatrix.from_logical(*logical_to_device(w_np, "fp16", device), g, dtype=torch.float16)
+    x64, x = make_x(oracle, rng, m, k, "fp16", device)
+    y = torch.empty((m, n), dtype=torch.float16, device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    ref = x64 @ oracle.weights_f64(*w_np, g, "fp16")
+    assert_close(oracle, host_f64(y), ref, "fp16", f"tiny scales M={m}")
+
+
 @pytest.mark.parametrize("group", [32, 64])
 @pytest.mark.parametrize("m", [1, 4, 16, 64])
 def test_linear_small_groups(oracle, hm, device, group, m):
