@@ -169,6 +169,7 @@ hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, i
     return e == hipSuccess ? HM_OK : hip_fail(e, "gemm launch");
 }
 
+// Workspace for any call of M rows over up to n columns (any column range within them) and kt_count K tiles.
 size_t linear_workspace(const hm::Planes &p, int64_t M, int64_t n, int64_t kt_count, bool fused) {
     if (M > kGemvMaxRows) {
         hm::GemmCall c;
@@ -185,7 +186,7 @@ size_t linear_workspace(const hm::Planes &p, int64_t M, int64_t n, int64_t kt_co
     c.n = n;
     c.kt_count = kt_count;
     c.fused = fused;
-    return hm::plan_gemv(c).partial_bytes;
+    return hm::gemv_partial_bound(c);
 }
 
 hm_status check_activation(const void *x, int64_t ldx, int64_t width, const char *what) {

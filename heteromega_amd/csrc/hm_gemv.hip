@@ -38,7 +38,10 @@ namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr size_t kXBudget = 64 * 1024; // staged activation bytes per workgroup (bounds the K range of a split)
+constexpr size_t kXBudget = 64 * 1024;   // staged activation bytes per workgroup at one row (bounds a split's K range)
+constexpr size_t kStageMax = 144 * 1024; // staged activation bytes per workgroup at several rows (LDS is 160 KiB)
+constexpr int64_t kCUs = 256;            // compute units of an MI355X
+constexpr int64_t kUnits = 7 * kCUs / 2; // (strip group, split) units a launch with several rows aims for
 
 struct GemvArgs {
     const uint4 *quant;
@@ -416,12 +419,25 @@ __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ part
     const int row = static_cast<int>(idx / nout);
     const int c = static_cast<int>(idx - static_cast<int64_t>(row) * nout);
     const int cg = FUSED ? (c >> 4) * 32 + (c & 15) : c; // gate (or plain) column
+    // Eight splits' loads are in flight at once (a load per split and a wait per add would put the splits'
+    // memory latencies in series); the sums still run in split order.
+    constexpr int kBatch = 8;
     float g = 0.0f, u = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-        const float *pr = partial + (static_cast<int64_t>(s) * m + row) * ncols + cg;
-        g += pr[0];
-        if constexpr (FUSED) {
-            u += pr[16];
+    for (int s0 = 0; s0 < splits; s0 += kBatch) {
+        float gv[kBatch], uv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int s = min(s0 + j, splits - 1); // past the last split: re-read it, not added
+            const float *pr = partial + (static_cast<int64_t>(s) * m + row) * ncols + cg;
+            gv[j] = pr[0];
+            uv[j] = FUSED ? pr[16] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            if (s0 + j < splits) {
+                g += gv[j];
+                u += uv[j];
+            }
         }
     }
     y[row * ldy + c] = T::from_float(FUSED ? silu(g) * u : g);
@@ -494,26 +510,62 @@ GemvPlan plan_gemv(const GemvCall &c) {
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
     p.spw = c.fused ? 2 : (c.m > 1 && strips % 2 == 0 ? 2 : 1);
     p.groups = strips / p.spw;
-    // K split: the staged activation chunk stays within kXBudget.
-    const int64_t max_tiles = std::max<int64_t>(1, static_cast<int64_t>(kXBudget) / (c.m * 256));
-    const int64_t splits0 = (c.kt_count + max_tiles - 1) / max_tiles;
-    p.kt_per_split = (c.kt_count + splits0 - 1) / splits0;
-    p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
-    // Waves per strip group: up to 8, keeping at least 8 K tiles per wave (16 with a strip pair at M = 1:
-    // measured on the Llama-3-8B gate_up, 32-tile wave runs in 448 workgroups beat 16-tile runs in 896).
-    const int64_t min_run = c.m == 1 ? 8 * p.spw : 8;
+    auto stage_bytes = [&](int64_t kts) {
+        const int64_t kc = kts * 128;
+        return static_cast<size_t>(c.m) * (kc + 8) * 2 + static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
+    };
+    auto set_splits = [&](int64_t splits) {
+        splits = std::min<int64_t>(std::max<int64_t>(splits, 1), c.kt_count);
+        p.kt_per_split = (c.kt_count + splits - 1) / splits;
+        p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
+    };
+    if (c.m == 1) {
+        // K split only to bound the staged chunk (kXBudget: 256 K tiles at one row).
+        const int64_t max_tiles = static_cast<int64_t>(kXBudget) / 256;
+        set_splits((c.kt_count + max_tiles - 1) / max_tiles);
+    } else {
+        // Several rows (launch shapes measured on the Llama-3-8B projections at M = 4 and 16, weights
+        // streamed from HBM): narrow grids (under 1.75 strip groups per CU) are split along K until there are
+        // 3.5 (strip group, split) units per CU; the staged chunk must leave room in LDS for the reduction.
+        set_splits(p.groups < kUnits / 2 ? (kUnits + p.groups - 1) / p.groups : 1);
+        while (stage_bytes(p.kt_per_split) > kStageMax && p.kt_per_split > 1) {
+            set_splits(p.splits + 1);
+        }
+    }
+    if (const int kts = env_int("HM_GEMV_KTS")) { // tuning override: K tiles per split
+        p.kt_per_split = std::min<int64_t>(kts, c.kt_count);
+        p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
+    }
     p.wps = 1;
-    while (p.wps < 8 && p.kt_per_split >= 2 * min_run * p.wps) {
-        p.wps *= 2;
-    }
-    // Strip groups per workgroup: at least 4 waves; with several rows, more groups share one staged chunk
-    // while the grid keeps at least one workgroup per CU.
     p.nu = 1;
-    while (p.nu * p.wps < 4) {
-        p.nu *= 2;
-    }
-    if (c.m > 1) {
-        while (p.nu * p.wps < 16 && ((p.groups + 2 * p.nu - 1) / (2 * p.nu)) * p.splits >= 256) {
+    if (c.m == 1) {
+        // Waves per strip group: up to 8, keeping at least 8 K tiles per wave (16 with a strip pair: measured
+        // on the Llama-3-8B gate_up, 32-tile wave runs in 448 workgroups beat 16-tile runs in 896); strip
+        // groups per workgroup: enough for 4 waves.
+        const int64_t min_run = 8 * p.spw;
+        while (p.wps < 8 && p.kt_per_split >= 2 * min_run * p.wps) {
+            p.wps *= 2;
+        }
+        while (p.nu * p.wps < 4) {
+            p.nu *= 2;
+        }
+    } else {
+        // 8 K tiles per wave and strip; workgroups of 8 to 16 waves, with enough strip groups that the staged
+        // chunk (M * 256 B per K tile) is at most half the workgroup's weight bytes (S KiB per K tile and group).
+        while (p.wps < 16 && p.kt_per_split >= 16 * p.wps) {
+            p.wps *= 2;
+        }
+        const int64_t nu_stage = (c.m + 2 * p.spw - 1) / (2 * p.spw);
+        while (p.nu * p.wps < 8 || p.nu < nu_stage) {
+            p.nu *= 2;
+        }
+        while (p.nu > 1 && p.nu * p.wps > 16) {
+            p.nu /= 2;
+        }
+        // From 8 rows, 16-wave workgroups share the chunk further while the grid keeps about one workgroup per
+        // CU (measured: faster at 8 and 16 rows, slower at 4).
+        const auto wgs = [&](int64_t nu) { return (p.groups + nu - 1) / nu * p.splits; };
+        while (c.m >= 8 && p.nu * p.wps < 16 && wgs(2 * p.nu) >= 27 * kCUs / 32) {
             p.nu *= 2;
         }
     }
@@ -530,6 +582,14 @@ GemvPlan plan_gemv(const GemvCall &c) {
     p.lds = std::max(stage, red);
     p.partial_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * c.m * strips * 16 * sizeof(float) : 0;
     return p;
+}
+
+size_t gemv_partial_bound(const GemvCall &c) {
+    // With several rows a range of fewer than kUnits / 2 strip groups takes ceil(kUnits / groups) splits,
+    // so splits * groups < 3 kUnits / 2; the staging-driven splits do not grow as the range narrows.
+    const GemvPlan p = plan_gemv(c);
+    const size_t narrow = c.m > 1 ? static_cast<size_t>(3 * kUnits / 2) * p.spw * c.m * 16 * sizeof(float) : 0;
+    return std::max(p.partial_bytes, narrow);
 }
 
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {

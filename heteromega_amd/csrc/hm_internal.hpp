@@ -64,6 +64,8 @@ struct GemvPlan {
     size_t partial_bytes = 0;
 };
 GemvPlan plan_gemv(const GemvCall &c);
+// The largest partial buffer of a call like c over any range of c's columns (narrower ranges split K more).
+size_t gemv_partial_bound(const GemvCall &c);
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream);
 
 // Prefill GEMM (MFMA 32x32x16) with the same operand conventions; fused writes SiLU(gate) * up.
