@@ -148,7 +148,8 @@ def prefill_bench(hm, torch, dev, layers, m, h, steps, warmup):
             L.forward(x, y, workspace=ws)
 
     g = graph_of(torch, run)
-    sec = time_graph(torch, g, max(1, steps // 2), 0.0, max(1, warmup // 2))
+    # Half a second of untimed replays first: the part's clock settles under sustained MFMA load.
+    sec = time_graph(torch, g, max(1, steps // 2), 0.5, max(1, warmup // 2))
     del L0
     return sec / 2
 
