@@ -446,13 +446,12 @@ __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ part
 template <class T, int MT, int G, int S, bool FUSED, int WGS>
 hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
     auto kern = gemv_kernel<T, MT, G, S, FUSED, WGS>;
-    static bool configured = false; // one attribute call per instantiation
-    if (!configured) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) {
-            return e;
-        }
-        configured = true;
+    // One attribute call per instantiation; a function-local static is initialized once even when several
+    // host threads launch at the same time.
+    static const hipError_t configured =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (configured != hipSuccess) {
+        return configured;
     }
     hipLaunchKernelGGL(kern, grid, dim3(WGS), lds, s, a);
     return hipGetLastError();

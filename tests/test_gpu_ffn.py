@@ -72,6 +72,11 @@ def test_ffn_qwen14b_group64(oracle, hm, device):
     y = layer.forward(x)
     torch.cuda.synchronize()
     assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, "fp16"), "fp16", "Qwen2.5-14B FFN g=64 decode")
+    for m in (8, 16):  # several-row decode: 16-wave workgroups, a K split of the gate_up, six of the down
+        x64, x = make_x(oracle, rng, m, 5120, "fp16", device)
+        y = layer.forward(x)
+        torch.cuda.synchronize()
+        assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, "fp16"), "fp16", f"Qwen2.5-14B FFN g=64 decode M={m}")
     x64, x = make_x(oracle, rng, 1024, 5120, "fp16", device)
     y = layer.forward(x)
     torch.cuda.synchronize()
