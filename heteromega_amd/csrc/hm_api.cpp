@@ -650,6 +650,81 @@ hm_status hm_ffn_forward(const hm_ffn *f, void *y, int64_t ldy, const void *x, i
     return hm_ffn_down(f, y, ldy, act, n, M, ch_begin, ch_end, rest, rest_bytes, stream);
 }
 
+size_t hm_ffn_block_workspace_bytes(const hm_ffn *f, int64_t max_m) {
+    if (f == nullptr || max_m <= 0) {
+        return 0;
+    }
+    // normed and y rows for the separate-kernel path, then the FFN's own workspace.
+    return 2 * static_cast<size_t>(round_up(max_m * f->hidden * 2, 256)) + hm_ffn_workspace_bytes(f, max_m);
+}
+
+hm_status hm_ffn_block_forward(const hm_ffn *f, void *x, int64_t ldx, const void *norm_weight, float eps, int64_t M, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+    if (f == nullptr || M <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_block_forward: null handle or M <= 0");
+    }
+    hm_status st = check_activation(x, ldx, f->hidden, "hm_ffn_block_forward x");
+    if (st != HM_OK) {
+        return st;
+    }
+    if (norm_weight == nullptr || !aligned(norm_weight, 16) || !(eps >= 0.0f)) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_block_forward: norm_weight must be 16-byte aligned and eps >= 0");
+    }
+    const size_t need = hm_ffn_block_workspace_bytes(f, M);
+    if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)) {
+        return fail(HM_WORKSPACE_TOO_SMALL, "hm_ffn_block_forward: workspace must be 256-byte aligned with >= %zu bytes (got %zu)", need,
+                    workspace_bytes);
+    }
+    const size_t rows_bytes = static_cast<size_t>(round_up(M * f->hidden * 2, 256));
+    uint16_t *normed = static_cast<uint16_t *>(workspace);
+    uint16_t *y = reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(workspace) + rows_bytes);
+    void *ffn_ws = static_cast<uint8_t *>(workspace) + 2 * rows_bytes;
+    const size_t ffn_bytes = workspace_bytes - 2 * rows_bytes;
+    const hipStream_t s = as_stream(stream);
+    const hm_dtype dtype = static_cast<hm_dtype>(f->gate_up.p.dtype);
+    if (M == 1 && f->hidden <= 8192) {
+        // Two launches: the gate_up GEMV stages RMSNorm(x) * weight, the down GEMV adds its output into x.
+        uint16_t *act = static_cast<uint16_t *>(ffn_ws);
+        const size_t act_bytes = static_cast<size_t>(round_up(f->inter * 2, 256));
+        hm::GemvCall c;
+        c.w = f->gate_up.p;
+        c.x = static_cast<const uint16_t *>(x);
+        c.ldx = ldx;
+        c.y = act;
+        c.ldy = f->inter;
+        c.m = 1;
+        c.n = f->inter;
+        c.kt_count = f->hidden / 128;
+        c.fused = true;
+        c.norm_w = static_cast<const uint16_t *>(norm_weight);
+        c.norm_eps = eps;
+        c.partial = reinterpret_cast<float *>(static_cast<uint8_t *>(ffn_ws) + act_bytes);
+        hipError_t e = hm::launch_gemv(c, s);
+        if (e != hipSuccess) {
+            return hip_fail(e, "block gate_up launch");
+        }
+        hm::GemvCall d;
+        d.w = f->down.p;
+        d.x = act;
+        d.ldx = f->inter;
+        d.y = static_cast<uint16_t *>(x);
+        d.ldy = ldx;
+        d.m = 1;
+        d.n = f->hidden;
+        d.kt_count = f->inter / 128;
+        d.accumulate = true;
+        d.partial = c.partial;
+        e = hm::launch_gemv(d, s);
+        return e == hipSuccess ? HM_OK : hip_fail(e, "block down launch");
+    }
+    // Several rows: RMSNorm, the FFN, the residual add (the same results as the two-launch path per row).
+    if ((st = hm_rmsnorm(normed, f->hidden, x, ldx, norm_weight, M, f->hidden, eps, dtype, stream)) != HM_OK ||
+        (st = hm_ffn_forward(f, y, f->hidden, normed, f->hidden, M, 0, f->inter, ffn_ws, ffn_bytes, stream)) != HM_OK) {
+        return st;
+    }
+    return hm_residual_add2(x, ldx, y, f->hidden, nullptr, 0, M, f->hidden, dtype, stream);
+}
+
 hm_status hm_silu_mul(const void *gate_up, int64_t ld_in, void *act, int64_t ld_out, int64_t rows, int64_t n, int32_t layout, hm_dtype dtype,
                       void *stream) {
     hm_status st = check_dtype(dtype);

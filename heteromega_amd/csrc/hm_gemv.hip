@@ -42,6 +42,7 @@ constexpr size_t kXBudget = 64 * 1024;   // staged activation bytes per workgrou
 constexpr size_t kStageMax = 144 * 1024; // staged activation bytes per workgroup at several rows (LDS is 160 KiB)
 constexpr int64_t kCUs = 256;            // compute units of an MI355X
 constexpr int64_t kUnits = 7 * kCUs / 2; // (strip group, split) units a launch with several rows aims for
+constexpr int kNormChunks = 4;           // RMSNorm in the staging: rows of up to 4 x 2048 columns
 
 struct GemvArgs {
     const uint4 *quant;
@@ -58,6 +59,10 @@ struct GemvArgs {
     int ncols; // 16 * strips of the call (row length of `partial`)
     int nu;    // strip groups per workgroup
     int wps;   // waves per strip group
+    // One row, whole K: the staged activation is RMSNorm(x) * norm_w (the norm of hm_rmsnorm, same rounding).
+    const uint16_t *norm_w;
+    float norm_eps;
+    bool accumulate; // plain output: y = round(y + round(sum)) (a residual add) instead of y = round(sum)
 };
 
 // v plus v of another lane of the same row of 16 (DPP control CTRL).
@@ -120,6 +125,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
     float2 *sums = reinterpret_cast<float2 *>(smem + static_cast<size_t>(m) * xst * 2);
     float *red = reinterpret_cast<float *>(smem);
+    const int norm_off = (m * xst * 2 + m * sst * static_cast<int>(sizeof(float2)) + 15) & ~15; // 4 floats past the staging
 
     // This wave's strip group and its contiguous run [tb, te) of the split's tiles. Groups past the end of
     // the call (a partial last workgroup) read the last group and are not stored.
@@ -152,13 +158,28 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int st_id = MT == 1 ? lane : tid;
     // Memory requests go out in this order: the activation chunks this thread stages (held in registers),
     // then the first KB steps of the wave's ring. Staging waits for the activations only.
-    uint4 xv[kPre];
+    // RMSNorm of the row (one row, whole K): waves 0..3 take the norm's chunks of the 256 threads of the
+    // separate RMSNorm kernel (thread t: elements 8t + 2048j), so its sum of squares is formed in the same order.
+    const bool norm = MT == 1 && a.norm_w != nullptr;
+    const int hcols = a.kt_count * 128;
+    uint4 nx[kNormChunks];
+    if (norm && wave < 4) {
+#pragma unroll
+        for (int j = 0; j < kNormChunks; ++j) {
+            const int c = (wave * 64 + lane) * 8 + j * 2048;
+            nx[j] = *reinterpret_cast<const uint4 *>(a.x + min(c, hcols - 8));
+        }
+    }
+    uint4 xv[kPre], wv[kPre] = {};
     auto fetch = [&](int base) { // branch-free: chunks past the end re-read a valid one and are not staged
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
             const int idx = st_hi > st_lo ? min(st_lo + base + c * st_step + st_id, st_hi - 1) : 0;
             const int row = MT == 1 ? 0 : idx / chunks_row;
             xv[c] = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
+            if (norm) {
+                wv[c] = *reinterpret_cast<const uint4 *>(a.norm_w + xk0 + idx * 8);
+            }
         }
     };
     fetch(0);
@@ -218,11 +239,56 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     __builtin_amdgcn_sched_barrier(0);
     advance();
 
+    float nscale = 1.0f;
+    if (norm) {
+        float *npart = reinterpret_cast<float *>(smem + norm_off);
+        if (wave < 4) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kNormChunks; ++j) {
+                const int c = (wave * 64 + lane) * 8 + j * 2048;
+                if (c < hcols) {
+                    const uint32_t w[4] = {nx[j].x, nx[j].y, nx[j].z, nx[j].w};
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const float v = T::to_float(k & 1 ? w[k >> 1] >> 16 : w[k >> 1] & 0xFFFFu);
+                        ss += v * v;
+                    }
+                }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                ss += __shfl_xor(ss, off);
+            }
+            if (lane == 0) {
+                npart[wave] = ss;
+            }
+        }
+        lds_barrier();
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            total += npart[w];
+        }
+        nscale = 1.0f / sqrtf(total / static_cast<float>(hcols) + a.norm_eps);
+    }
+
     // 1. Stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes take
     //    consecutive 8-element chunks of a row, so one group is G / 8 consecutive lanes.
-    auto stage = [&](int idx, uint4 v, bool valid) {
+    auto stage = [&](int idx, uint4 v, uint4 g, bool valid) {
         float sa = 0.0f, sb = 0.0f;
         int row = 0, c8 = 0;
+        if (norm) { // v <- round(v * scale * g) element-wise, as the RMSNorm kernel stores it
+            uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float lo = T::to_float(vw[i] & 0xFFFFu) * nscale * T::to_float(gw[i] & 0xFFFFu);
+                const float hi = T::to_float(vw[i] >> 16) * nscale * T::to_float(gw[i] >> 16);
+                vw[i] = static_cast<uint32_t>(T::from_float(lo)) | (static_cast<uint32_t>(T::from_float(hi)) << 16);
+            }
+            v = uint4{vw[0], vw[1], vw[2], vw[3]};
+        }
         if (valid) {
             row = MT == 1 ? 0 : idx / chunks_row;
             c8 = idx - row * chunks_row;
@@ -263,14 +329,14 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 #pragma unroll
     for (int c = 0; c < kPre; ++c) {
         const int idx = st_lo + c * st_step + st_id;
-        stage(idx, xv[c], idx < st_hi); // all lanes take part in the shuffles
+        stage(idx, xv[c], wv[c], idx < st_hi); // all lanes take part in the shuffles
     }
     for (int base = kPre * st_step; st_lo + base < st_hi; base += kPre * st_step) {
         fetch(base); // long ranges only: these chunks wait behind the first ring steps
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
             const int idx = st_lo + base + c * st_step + st_id;
-            stage(idx, xv[c], idx < st_hi);
+            stage(idx, xv[c], wv[c], idx < st_hi);
         }
     }
     if constexpr (MT == 1) {
@@ -401,7 +467,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         } else if constexpr (FUSED) {
             a.y[row * a.ldy + gg * 16 + c] = T::from_float(silu(v[0]) * v[1]);
         } else {
-            a.y[row * a.ldy + (gg * S + s_out) * 16 + c] = T::from_float(v[s_out]);
+            uint16_t *yp = a.y + row * a.ldy + (gg * S + s_out) * 16 + c;
+            const uint16_t yv = T::from_float(v[s_out]);
+            *yp = a.accumulate ? T::from_float(T::to_float(*yp) + T::to_float(yv)) : yv;
         }
     }
 }
@@ -410,7 +478,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 // output is SiLU(gate) * up per channel (ncols / 2 channels).
 template <class T, bool FUSED>
 __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ partial, uint16_t *__restrict__ y, int64_t ldy, int m,
-                                                  int ncols, int splits) {
+                                                  int ncols, int splits, bool accumulate) {
     const int nout = FUSED ? ncols / 2 : ncols;
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= static_cast<int64_t>(m) * nout) {
@@ -440,7 +508,8 @@ __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ part
             }
         }
     }
-    y[row * ldy + c] = T::from_float(FUSED ? silu(g) * u : g);
+    const uint16_t out = T::from_float(FUSED ? silu(g) * u : g);
+    y[row * ldy + c] = accumulate ? T::from_float(T::to_float(y[row * ldy + c]) + T::to_float(out)) : out;
 }
 
 template <class T, int MT, int G, int S, bool FUSED, int WGS>
@@ -578,7 +647,8 @@ GemvPlan plan_gemv(const GemvCall &c) {
     const int64_t kc = p.kt_per_split * 128;
     const size_t stage = static_cast<size_t>(c.m) * (kc + 8) * 2 + static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
     const size_t red = static_cast<size_t>(p.waves) * p.spw * c.m * 16 * sizeof(float);
-    p.lds = std::max(stage, red);
+    // One row may also hold the RMSNorm's four partial sums past the staging area.
+    p.lds = std::max(((stage + 15) & ~static_cast<size_t>(15)) + (c.m == 1 ? 16 : 0), red);
     p.partial_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * c.m * strips * 16 * sizeof(float) : 0;
     return p;
 }
@@ -614,6 +684,9 @@ hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
     a.ncols = static_cast<int>(p.groups * p.spw * 16);
     a.nu = p.nu;
     a.wps = p.wps;
+    a.norm_w = c.norm_w;
+    a.norm_eps = c.norm_eps;
+    a.accumulate = c.accumulate;
     const dim3 grid(static_cast<unsigned>((p.groups + p.nu - 1) / p.nu), static_cast<unsigned>(p.splits));
     const int group = static_cast<int>(c.w.group);
     hipError_t e = c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream)
@@ -621,25 +694,25 @@ hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
     if (e != hipSuccess || p.splits == 1) {
         return e;
     }
-    return launch_sum_splits(c.partial, c.y, c.ldy, c.m, a.ncols, static_cast<int>(p.splits), c.fused, c.w.dtype, stream);
+    return launch_sum_splits(c.partial, c.y, c.ldy, c.m, a.ncols, static_cast<int>(p.splits), c.fused, c.w.dtype, stream, c.accumulate);
 }
 
 hipError_t launch_sum_splits(const float *partial, uint16_t *y, int64_t ldy, int64_t m, int ncols, int splits, bool fused,
-                             int dtype, hipStream_t stream) {
+                             int dtype, hipStream_t stream, bool accumulate) {
     const int64_t total = m * (fused ? ncols / 2 : ncols);
     const dim3 blocks(static_cast<unsigned>((total + 255) / 256));
     const int mi = static_cast<int>(m);
     if (dtype == 1) {
         if (fused) {
-            hipLaunchKernelGGL((sum_splits<F16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
+            hipLaunchKernelGGL((sum_splits<F16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
         } else {
-            hipLaunchKernelGGL((sum_splits<F16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
+            hipLaunchKernelGGL((sum_splits<F16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
         }
     } else {
         if (fused) {
-            hipLaunchKernelGGL((sum_splits<BF16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
+            hipLaunchKernelGGL((sum_splits<BF16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
         } else {
-            hipLaunchKernelGGL((sum_splits<BF16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits);
+            hipLaunchKernelGGL((sum_splits<BF16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
         }
     }
     return hipGetLastError();

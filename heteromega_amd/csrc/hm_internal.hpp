@@ -52,6 +52,10 @@ struct GemvCall {
     int64_t kt_begin = 0, kt_count = 0;
     bool fused = false;
     float *partial = nullptr; // split-K partials (GemvPlan::partial_bytes)
+    // One row over the whole K (kt_begin 0, K <= 8192): stage RMSNorm(x) * norm_w instead of x.
+    const uint16_t *norm_w = nullptr;
+    float norm_eps = 0.0f;
+    bool accumulate = false; // plain output: y = round(y + round(x W)) (residual add into y)
 };
 // Launch shape of a GemvCall: strips per wave, strip groups, K split, waves per strip group, strip groups per
 // workgroup, LDS bytes and the fp32 partial buffer the split needs (0 without a split).
@@ -96,7 +100,7 @@ hipError_t launch_gemm(const GemmCall &c, hipStream_t stream);
 // Adds split-K partials [splits][m][ncols] into y [m, ncols] (or, fused, y [m, ncols / 2] = SiLU(gate) * up
 // with gate and up alternating per 16 columns).
 hipError_t launch_sum_splits(const float *partial, uint16_t *y, int64_t ldy, int64_t m, int ncols, int splits, bool fused,
-                             int dtype, hipStream_t stream);
+                             int dtype, hipStream_t stream, bool accumulate = false);
 
 hipError_t launch_silu_mul(const uint16_t *gate_up, int64_t ld_in, uint16_t *act, int64_t ld_out, int64_t rows, int64_t n,
                            bool interleaved, int dtype, hipStream_t stream);

@@ -364,6 +364,29 @@ class FfnLayer:
         _call(_lib.load().hm_ffn_forward(self._h, _ptr(y), y.stride(0), _ptr(x), x.stride(0), m, b, e, wp, wb, _stream(stream, x.device)))
         return y
 
+    def block_workspace_bytes(self, max_m):
+        return _lib.load().hm_ffn_block_workspace_bytes(self._h, max_m)
+
+    def block_forward(self, x, norm_weight, eps=1e-5, stream=None, workspace=None):
+        """In place: x [M, H] += FFN(RMSNorm(x) * norm_weight), the pre-norm FFN block of a layer stack
+        (unified_llm_w4a16.cpp:2867-2892 with the layer-boundary norm and residual of residual_norm.cu:25-98).
+
+        Equal bit for bit to rmsnorm, forward and residual_add2 in sequence; one row runs as two launches."""
+        if norm_weight.numel() != self.hidden or norm_weight.dtype != x.dtype or not norm_weight.is_contiguous():
+            raise ValueError(f"norm_weight must be a contiguous {x.dtype} vector of {self.hidden} elements")
+        m = x.size(0)
+        need = self.block_workspace_bytes(m)
+        if workspace is None:
+            key = ("block", _stream(stream, self.device).value)
+            workspace = self._ws.get(key)
+            if workspace is None or workspace.numel() < need + 256:
+                workspace = torch.empty(need + 256, dtype=torch.uint8, device=self.device)
+                self._ws[key] = workspace
+        wp, wb = _aligned(workspace, need)
+        _call(_lib.load().hm_ffn_block_forward(self._h, _ptr(x), x.stride(0), _ptr(norm_weight), eps, m, wp, wb,
+                                               _stream(stream, x.device)))
+        return x
+
     def gate_up(self, x, act=None, channels=None, stream=None):
         b, e = self._channels(channels)
         m = x.size(0)

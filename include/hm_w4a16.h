@@ -193,6 +193,18 @@ hm_status hm_ffn_gate_up(const hm_ffn *f, void *act, int64_t ld_act, const void 
 hm_status hm_ffn_down(const hm_ffn *f, void *y, int64_t ldy, const void *act, int64_t ld_act, int64_t M,
                       int64_t ch_begin, int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream);
 
+/* Workspace for hm_ffn_block_forward with up to max_m rows. */
+size_t hm_ffn_block_workspace_bytes(const hm_ffn *f, int64_t max_m);
+
+/* One pre-norm FFN block of a layer stack, in place: x [M, H] (ldx) += FFN(RMSNorm(x) * norm_weight), eps as in
+ * hm_rmsnorm. This is the model's FFN block with the layer-boundary norm and residual add
+ * (src/unified_llm_w4a16_hetero/unified_llm_w4a16.cpp:2867-2892 with kernels/gpu/src/residual_norm.cu:25-98).
+ * One row (H <= 8192) runs as two launches: the gate_up GEMV normalizes x while staging it and the down GEMV
+ * adds its rounded output into x. Other M run hm_rmsnorm, hm_ffn_forward and hm_residual_add2. Either way the
+ * result equals those three calls bit for bit. Needs hm_ffn_block_workspace_bytes(f, M) bytes of workspace. */
+hm_status hm_ffn_block_forward(const hm_ffn *f, void *x, int64_t ldx, const void *norm_weight, float eps, int64_t M,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Elementwise operators next to the FFN.
  * ------------------------------------------------------------------------- */

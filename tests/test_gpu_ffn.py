@@ -281,3 +281,32 @@ def test_ffn_stack_decode_small(oracle, hm, device):
         torch.cuda.synchronize()
         assert_close(oracle, host_f64(x), ref, dtype, "stack step")
         ref = host_f64(x)  # re-anchor each step so rounding flips do not compound
+
+
+@pytest.mark.parametrize("m", [1, 4, 37])
+@pytest.mark.parametrize("dtype,hidden,inter,group", [("fp16", 4096, 14336, 128), ("bf16", 4096, 14336, 128), ("fp16", 5120, 13824, 64)])
+def test_block_forward_equals_separate_ops(oracle, hm, device, dtype, hidden, inter, group, m):
+    # x += FFN(RMSNorm(x) * w) in place. One row: the gate_up GEMV normalizes x while staging it and the down GEMV
+    # adds its rounded output into x (two launches); other M run the separate kernels. Either way the bits equal
+    # rmsnorm, forward and residual_add2 in sequence (the layer boundary of residual_norm.cu:25-98).
+    layer, _, wf = _layer(oracle, hm, device, hidden, inter, group, dtype, 5)
+    rng = np.random.default_rng(110 + m)
+    x64, x = make_x(oracle, rng, m, hidden, dtype, device)
+    w = (torch.from_numpy(rng.uniform(0.5, 1.5, hidden).astype(np.float32)).to(device)).to(TORCH[dtype])
+    ref = x.clone()
+    normed = torch.empty_like(x)
+    hm.rmsnorm(normed, ref, w, 1e-5)
+    y = layer.forward(normed)
+    hm.residual_add2(ref, y)
+    got = x.clone()
+    for rep in range(2):  # the second call reuses the cached workspace
+        got.copy_(x)
+        layer.block_forward(got, w, 1e-5)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), (dtype, hidden, m, rep)
+    if m == 1:  # and against the float64 oracle with the same rounding points
+        w64 = host_f64(w.view(1, -1))[0]
+        nr = oracle.round_to(oracle.rmsnorm(x64, w64, 1e-5).astype(np.float32), dtype).astype(np.float64)
+        yr = oracle.round_to(_ffn_ref(oracle, nr, wf, dtype).astype(np.float32), dtype).astype(np.float64)
+        assert_close(oracle, host_f64(got), oracle.round_to((x64 + yr).astype(np.float32), dtype).astype(np.float64), dtype,
+                     "FFN block M=1")
