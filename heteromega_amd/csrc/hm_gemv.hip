@@ -617,6 +617,11 @@ GemvPlan plan_gemv(const GemvCall &c) {
         while (p.nu * p.wps < 4) {
             p.nu *= 2;
         }
+        // Between one and two strip groups per CU (Qwen2.5-14B down: 320 strips), workgroups of twice the strips
+        // run one round on fewer CUs: measured 11.2 µs against 12.1 µs for 320 workgroups.
+        if (!c.fused && p.groups > kCUs && p.groups < 2 * kCUs && p.nu * p.wps <= 8) {
+            p.nu *= 2;
+        }
     } else {
         // 8 K tiles per wave and strip; workgroups of 8 to 16 waves, with enough strip groups that the staged
         // chunk (M * 256 B per K tile) is at most half the workgroup's weight bytes (S KiB per K tile and group).
