@@ -130,7 +130,7 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds
 #endif
 }
 
-template <class T, int G, bool FUSED, int RBW, int NSW, int WN>
+template <class T, int G, bool FUSED, int RBW, int NSW, int WN, int DEPTH>
 __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2))) gemm_kernel(GemmArgs a) {
     constexpr int WGS = WN * 64;
     constexpr int BM = RBW * 16;
@@ -139,12 +139,21 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     constexpr int SPG = 4 / GPT;       // 32-K steps per group
     constexpr int ADMA = BM * 16 / WGS; // 1 KiB activation transfers per wave per K tile
     static_assert(ADMA * WGS == BM * 16, "activation transfers");
+    // K tiles in flight: DEPTH - 1 tiles ahead of the one being multiplied, each with its weights in registers
+    // and its activations in one of DEPTH LDS buffers. Per K tile a wave issues NB weight/record loads and ADMA
+    // activation transfers, in that order; all of them count in vmcnt, in order.
+    static_assert(DEPTH == 2 || DEPTH == 4, "pipeline depth");
+    constexpr int NB = 2 * NSW;
+    constexpr int AHEAD = (DEPTH - 2) * (NB + ADMA); // loads issued after tile kt + 1's activations at iteration kt
     // Activation tile of one K tile: BM rows of 128 halves (256 B), 16-byte chunks XOR-swizzled by row
     // (chunk c of row r at slot c ^ (r % 16)), so the 16 rows one MFMA operand read touches fall on distinct banks.
     // Two separate arrays (not one [2][...]) so that the compiler can tell the buffers apart and does not
     // make reads of one wait for the transfers into the other.
     __shared__ __align__(1024) uint8_t as0[BM * 256];
     __shared__ __align__(1024) uint8_t as1[BM * 256];
+    __shared__ __align__(1024) uint8_t as2[DEPTH > 2 ? BM * 256 : 16];
+    __shared__ __align__(1024) uint8_t as3[DEPTH > 2 ? BM * 256 : 16];
+    auto abuf = [&](int buf) __attribute__((always_inline)) { return buf == 0 ? as0 : buf == 1 ? as1 : buf == 2 ? as2 : as3; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -216,7 +225,7 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
         const uint32_t so = static_cast<uint32_t>(kt) * 256u;
 #pragma unroll
         for (int j = 0; j < ADMA; ++j) {
-            lds_dma16(xr, (buf ? as1 : as0) + (wave * ADMA + j) * 1024, xoff[j], so);
+            lds_dma16(xr, abuf(buf) + (wave * ADMA + j) * 1024, xoff[j], so);
         }
     };
 
@@ -251,20 +260,22 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     // Fragment of row block rb, step mu: row rb * 16 + col, chunk 4 mu + h at its swizzled slot.
     const uint32_t aread = static_cast<uint32_t>(col) * 256u;
     auto read_a = [&](int buf, int mu, AFr &f) __attribute__((always_inline)) {
-        const uint8_t *ab = (buf ? as1 : as0) + aread + (((4 * mu + h) ^ col) << 4);
+        const uint8_t *ab = abuf(buf) + aread + (((4 * mu + h) ^ col) << 4);
 #pragma unroll
         for (int rb = 0; rb < RBW; ++rb) {
             f.v[rb] = *reinterpret_cast<const uint4 *>(ab + rb * 4096);
         }
     };
 
-    // One K tile. On entry `op` holds step 0's B operands of `cur`, `dq` the constants of `cur`, `fa` step 0's
-    // activation fragments; on exit the same for K tile kt + 1.
-    auto iteration = [&](int kt, int buf, const BTile<T, G, NSW> &cur, BTile<T, G, NSW> &nxt, Deq<T> (&dq)[NSW], BOps &op,
-                         AFr &fa) __attribute__((always_inline)) {
-        const int ktn = min(kt + 1, nkt - 1); // the last iteration re-requests its own tile; nothing reads it
-        load_b(ktn, nxt);
-        load_a(ktn, buf ^ 1); // that buffer was last read before the previous barrier
+    // One K tile in pipeline slot `buf` (kt % DEPTH). On entry `op` holds step 0's B operands of `cur`, `dq` the
+    // constants of `cur`, `fa` step 0's activation fragments; on exit the same for K tile kt + 1 (slot `nb`). The
+    // tile DEPTH - 1 ahead goes into slot `lb` (that of K tile kt - 1, whose registers and LDS buffer were last
+    // read before the previous barrier).
+    auto iteration = [&](int kt, int buf, int nb, const BTile<T, G, NSW> &cur, const BTile<T, G, NSW> &nxt, BTile<T, G, NSW> &ld, int lb,
+                         Deq<T> (&dq)[NSW], BOps &op, AFr &fa) __attribute__((always_inline)) {
+        const int ktn = min(kt + DEPTH - 1, nkt - 1); // the last iterations re-request the last tile; nothing reads it
+        load_b(ktn, ld);
+        load_a(ktn, lb);
 #pragma unroll
         for (int mu = 0; mu < 4; ++mu) {
             BOps on;
@@ -273,7 +284,7 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
                 read_a(buf, mu + 1, fn);
                 dequant_step(cur, dq, mu + 1, on);
             } else {
-                wait_vmcnt<ADMA>(); // nxt's weights (the activation transfers behind them may still run)
+                wait_vmcnt<ADMA + AHEAD>(); // nxt's weights (the transfers issued after them may still run)
                 dequant_step(nxt, dq, 0, on);
             }
             // strip-major: the operand of the last strip, finished at the end of the previous step, is needed last
@@ -296,28 +307,38 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
             }
         }
         // The next tile's activations: this wave's transfers done, then everyone's.
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        read_a(buf ^ 1, 0, fa);
+        wait_vmcnt<AHEAD>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        read_a(nb, 0, fa);
     };
 
-    BTile<T, G, NSW> b0, b1;
-    load_b(0, b0);
-    load_a(0, 0);
+    BTile<T, G, NSW> b[DEPTH];
+#pragma unroll
+    for (int t = 0; t + 1 < DEPTH; ++t) {
+        load_b(min(t, nkt - 1), b[t]);
+        load_a(min(t, nkt - 1), t);
+    }
     Deq<T> dq[NSW];
     BOps op;
     AFr fa;
-    wait_vmcnt<ADMA>();
-    dequant_step(b0, dq, 0, op);
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    wait_vmcnt<ADMA + AHEAD>();
+    dequant_step(b[0], dq, 0, op);
+    wait_vmcnt<AHEAD>();
+    asm volatile("s_barrier" ::: "memory");
     read_a(0, 0, fa);
-    // Two K tiles per trip, so the register sets alternate without copies.
+    // DEPTH K tiles per trip, so the register sets and LDS buffers rotate without copies.
     int kt = 0;
-    for (; kt + 1 < nkt; kt += 2) {
-        iteration(kt, 0, b0, b1, dq, op, fa);
-        iteration(kt + 1, 1, b1, b0, dq, op, fa);
+    for (; kt + DEPTH - 1 < nkt; kt += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; ++u) {
+            iteration(kt + u, u, (u + 1) % DEPTH, b[u], b[(u + 1) % DEPTH], b[(u + DEPTH - 1) % DEPTH], (u + DEPTH - 1) % DEPTH, dq, op, fa);
+        }
     }
-    if (kt < nkt) {
-        iteration(kt, 0, b0, b1, dq, op, fa);
+#pragma unroll
+    for (int u = 0; u + 1 < DEPTH; ++u) {
+        if (kt + u < nkt) {
+            iteration(kt + u, u, (u + 1) % DEPTH, b[u], b[(u + 1) % DEPTH], b[(u + DEPTH - 1) % DEPTH], (u + DEPTH - 1) % DEPTH, dq, op, fa);
+        }
     }
 
     // Epilogue through a buffer covering this tile's valid rows: stores of rows past M fall outside it and are
@@ -346,11 +367,11 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     }
 }
 
-template <class T, int G, int RBW, int NSW, int WN> hipError_t launch_cfg(const GemmArgs &a, bool fused, dim3 grid, hipStream_t s) {
+template <class T, int G, int RBW, int NSW, int WN, int DEPTH> hipError_t launch_cfg(const GemmArgs &a, bool fused, dim3 grid, hipStream_t s) {
     if (fused) {
-        hipLaunchKernelGGL((gemm_kernel<T, G, true, RBW, NSW, WN>), grid, dim3(WN * 64), 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel<T, G, true, RBW, NSW, WN, DEPTH>), grid, dim3(WN * 64), 0, s, a);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<T, G, false, RBW, NSW, WN>), grid, dim3(WN * 64), 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel<T, G, false, RBW, NSW, WN, DEPTH>), grid, dim3(WN * 64), 0, s, a);
     }
     return hipGetLastError();
 }
@@ -358,9 +379,9 @@ template <class T, int G, int RBW, int NSW, int WN> hipError_t launch_cfg(const 
 template <class T, int G> hipError_t launch_g(const GemmArgs &a, bool fused, int cfg, dim3 grid, hipStream_t s) {
     switch (cfg) {
     case 1:
-        return launch_cfg<T, G, 8, 2, 4>(a, fused, grid, s); // 128 x 128, 4 waves of 128 x 32
+        return launch_cfg<T, G, 8, 2, 4, 2>(a, fused, grid, s); // 128 x 128, 4 waves of 128 x 32, 1 K tile ahead
     default:
-        return launch_cfg<T, G, 4, 2, 4>(a, fused, grid, s); // 64 x 128, 4 waves of 64 x 32
+        return launch_cfg<T, G, 4, 2, 4, 4>(a, fused, grid, s); // 64 x 128, 4 waves of 64 x 32, 3 K tiles ahead
     }
 }
 
