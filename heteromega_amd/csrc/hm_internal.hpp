@@ -86,8 +86,8 @@ struct GemmCall {
     bool fused = false;
     float *partial = nullptr; // split-K partials (GemmPlan::partial_bytes)
 };
-// Tile configuration (1: 128 x 128 tiles, 0: 64 x 128, 4 waves each). The GEMM does not split K (splits = 1,
-// no partials); the fields keep the GEMV's plan shape.
+// Tile configuration (2: 128 x 256 tiles, 8 waves; 1: 128 x 128, 4 waves; 0: 64 x 128, 4 waves). The GEMM does
+// not split K (splits = 1, no partials); the fields keep the GEMV's plan shape.
 struct GemmPlan {
     int cfg = 1;
     int64_t tiles_m = 0, tiles_n = 0;
