@@ -57,6 +57,53 @@ def make_layers(hm, torch, dev, h, i, g, count, dtype=None, seed=0):
     return layers
 
 
+def qkv_bench(hm, torch, dev, h, g, sets=24):
+    """Q, K, V projections of one attention block: three launches against one on the concatenated matrix."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    widths = (h, h // 4, h // 4)
+    parts, fused = [], []
+    for _ in range(sets):
+        mats = []
+        for n in widths:
+            q = torch.randint(0, 16, (h, n), dtype=torch.uint8, device=dev, generator=gen)
+            s = (torch.rand((h // g, n), device=dev, generator=gen) * 0.019 + 0.001).to(torch.float16)
+            z = torch.randint(0, 16, (h // g, n), dtype=torch.uint8, device=dev, generator=gen)
+            mats.append(hm.RepackedMatrix.from_logical(q, s, z, g, dtype=torch.float16))
+        parts.append(mats)
+        fused.append(hm.RepackedMatrix.concat(mats))
+    torch.cuda.synchronize()
+    n_all = sum(widths)
+    out = {}
+    for m, count in ((1, sets), (2048, 2)):
+        x = torch.randn((m, h), device=dev).to(torch.float16)
+        y = torch.empty((m, n_all), device=dev, dtype=torch.float16)
+        ws = torch.empty(max(parts[0][0].workspace_bytes(m), fused[0].workspace_bytes(m)) + 512, dtype=torch.uint8, device=dev)
+
+        def separate():
+            for mats in parts[:count]:
+                c0 = 0
+                for w in mats:
+                    hm.packed_linear(y[:, c0:c0 + w.n], x, w, workspace=ws)
+                    c0 += w.n
+
+        def one():
+            for w in fused[:count]:
+                hm.packed_linear(y, x, w, workspace=ws)
+
+        t_sep = time_graph(torch, graph_of(torch, separate), 20, 0.3, 2) / count
+        t_one = time_graph(torch, graph_of(torch, one), 20, 0.3, 2) / count
+        if m == 1:
+            b = h * n_all // 2 + (h // g) * n_all * 3
+            out["decode_M1"] = {"us_three_launches": round(t_sep * 1e6, 2), "us_one_launch": round(t_one * 1e6, 2),
+                                "GB_s_one_launch": round(b / t_one / 1e9, 1)}
+        else:
+            f = 2.0 * m * h * n_all
+            out[f"prefill_M{m}"] = {"us_three_launches": round(t_sep * 1e6, 1), "us_one_launch": round(t_one * 1e6, 1),
+                                    "TFLOP_s_one_launch": round(f / t_one / 1e12, 1)}
+    return out
+
+
 def graph_of(torch, fn):
     """Captures fn() (enqueueing on the current stream) into a HIP graph after one eager warm-up call."""
     s = torch.cuda.Stream()
@@ -348,6 +395,11 @@ def main():
         log(f"32-layer stack: {tok * 1e6:.1f} us/token")
         del stack, gt
         torch.cuda.empty_cache()
+
+        # Attention Q/K/V projections through the same operator (Llama-3-8B: 4096 -> 4096 + 1024 + 1024): three
+        # launches against one launch on the concatenated matrix. 24 weight sets (300 MB) rotate at M = 1.
+        extra["attention_qkv"] = qkv_bench(hm, torch, dev, H, G)
+        log(f"attention QKV: {extra['attention_qkv']}")
 
         # Qwen2.5-14B FFN shape, group 64.
         qh, qi, qg = 5120, 13824, 64

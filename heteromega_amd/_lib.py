@@ -62,6 +62,7 @@ _SIGNATURES = {
                                        ctypes.POINTER(I64)]),
     "hm_weights_planes": (ctypes.c_int, [P, ctypes.POINTER(P), ctypes.POINTER(I64), ctypes.POINTER(P), ctypes.POINTER(I64)]),
     "hm_weights_destroy": (ctypes.c_int, [P]),
+    "hm_weights_concat": (ctypes.c_int, [ctypes.POINTER(P), ctypes.c_int32, P, ctypes.POINTER(P)]),
     "hm_linear_workspace_bytes": (SZ, [P, I64, I64, I64]),
     "hm_linear": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I64, I64, P, SZ, P]),
     "hm_ffn_from_tiles": (ctypes.c_int, [P, P, P, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),

@@ -419,6 +419,55 @@ hm_status hm_weights_destroy(hm_weights *w) {
     return HM_OK;
 }
 
+hm_status hm_weights_concat(const hm_weights *const *parts, int32_t count, void *stream, hm_weights **out) {
+    if (out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_concat: null output handle");
+    }
+    *out = nullptr;
+    if (parts == nullptr || count <= 0) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_concat: no parts");
+    }
+    int64_t n = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const hm_weights *w = parts[i];
+        if (w == nullptr) {
+            return fail(HM_INVALID_ARGUMENT, "hm_weights_concat: part %d is null", static_cast<int>(i));
+        }
+        if (w->p.K != parts[0]->p.K || w->p.group != parts[0]->p.group || w->p.dtype != parts[0]->p.dtype) {
+            return fail(HM_INVALID_ARGUMENT, "hm_weights_concat: part %d has K %lld, group %lld, dtype %d; part 0 has %lld, %lld, %d",
+                        static_cast<int>(i), static_cast<long long>(w->p.K), static_cast<long long>(w->p.group), w->p.dtype,
+                        static_cast<long long>(parts[0]->p.K), static_cast<long long>(parts[0]->p.group), parts[0]->p.dtype);
+        }
+        n += w->p.N;
+    }
+    auto *c = new hm_weights;
+    hm_status st = alloc_planes(c, parts[0]->p.K, n, parts[0]->p.group, parts[0]->p.dtype);
+    if (st != HM_OK) {
+        delete c;
+        return st;
+    }
+    // Both planes are strip-major (a strip's K tiles, then the next strip), so the parts' planes concatenate.
+    int64_t qo = 0, mo = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const hm_weights *w = parts[i];
+        hipError_t e = hipMemcpyAsync(const_cast<uint8_t *>(c->p.quant) + qo, w->p.quant, static_cast<size_t>(w->quant_bytes),
+                                      hipMemcpyDeviceToDevice, as_stream(stream));
+        if (e == hipSuccess) {
+            e = hipMemcpyAsync(reinterpret_cast<uint8_t *>(const_cast<uint32_t *>(c->p.meta)) + mo, w->p.meta,
+                               static_cast<size_t>(w->meta_bytes), hipMemcpyDeviceToDevice, as_stream(stream));
+        }
+        if (e != hipSuccess) {
+            free_planes(c);
+            delete c;
+            return hip_fail(e, "hm_weights_concat copy");
+        }
+        qo += w->quant_bytes;
+        mo += w->meta_bytes;
+    }
+    *out = c;
+    return HM_OK;
+}
+
 size_t hm_linear_workspace_bytes(const hm_weights *w, int64_t M, int64_t k, int64_t n) {
     if (w == nullptr || M <= 0 || k <= 0 || n <= 0) {
         return 0;

@@ -180,6 +180,18 @@ class RepackedMatrix:
                                                   _stream(stream, q.device), ctypes.byref(h)))
         return cls(h, q.device)
 
+    @classmethod
+    def concat(cls, parts, stream=None):
+        """The columns of matrices with the same K, group and dtype side by side, [K, sum of N]: an attention
+        block's Q, K and V projections as one launch (the reference reuses only the prepared input,
+        GemmInputReuse, gpu_ffn.hpp:117-127). The parts stay valid and owned by the caller."""
+        if not parts:
+            raise ValueError("concat: no parts")
+        arr = (ctypes.c_void_p * len(parts))(*[p._h for p in parts])
+        h = ctypes.c_void_p()
+        _call(_lib.load().hm_weights_concat(arr, len(parts), _stream(stream, parts[0].device), ctypes.byref(h)))
+        return cls(h, parts[0].device)
+
     def to_logical(self, stream=None):
         q = torch.empty((self.k, self.n), dtype=torch.uint8, device=self.device)
         s = torch.empty((self.k // self.group, self.n), dtype=self.dtype, device=self.device)

@@ -129,6 +129,14 @@ hm_status hm_weights_planes(const hm_weights *w, const void **quant, int64_t *qu
 
 hm_status hm_weights_destroy(hm_weights *w);
 
+/* Columns of `count` matrices with the same K, group and dtype side by side in one new matrix
+ * [K, N_0 + N_1 + ...], so projections that read the same input (an attention block's Q, K and V) run as one
+ * hm_linear launch whose output holds their columns in order. The reference reads the input of Q, K and V
+ * three times and reuses only its prepared GEMM layout (GemmInputReuse, kernels/gpu/include/heteromega/
+ * gpu_ffn.hpp:117-127; QuantizedLinear calls at src/unified_llm_w4a16_hetero/unified_llm_w4a16.cpp:2795).
+ * The parts are copied (device to device on `stream`) and stay owned by the caller. */
+hm_status hm_weights_concat(const hm_weights *const *parts, int32_t count, void *stream, hm_weights **out);
+
 /* ---------------------------------------------------------------------------
  * One projection: y[M, n] = x[M, k] @ W[:k, :n].
  * Replaces hipkernels::w4a16_gemv_fused_packed / w4a16_gemm_fused_packed[_tiles]

@@ -162,3 +162,30 @@ def test_constant_input_exact(oracle, hm, device):
             hm.packed_linear(y, x, w)
             torch.cuda.synchronize()
             assert torch.all(y.float() == 8.0), (dt, m)
+
+
+@pytest.mark.parametrize("m", [1, 8, 37, 512])
+def test_concat_qkv_equals_separate(oracle, hm, device, m):
+    # The Q, K and V projections of a Llama-3-8B attention block (grouped K/V: 4096, 1024 and 1024 columns) as
+    # one matrix and one launch. Bit for bit against three launches at one row and on the GEMM path (an output
+    # column's sum does not depend on the other columns there); within tolerance at 2..16 rows, where the K
+    # split follows the matrix width. The concatenated planes decode to the parts' logical tensors side by side.
+    rng = np.random.default_rng(120)
+    k, g, dtype = 4096, 128, "fp16"
+    parts = [_matrix(oracle, hm, rng, k, n, g, dtype, device) for n in (4096, 1024, 1024)]
+    qkv = hm.RepackedMatrix.concat([w for _, w in parts])
+    assert (qkv.k, qkv.n, qkv.group) == (k, 6144, g)
+    q, s, z = qkv.to_logical()
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), np.concatenate([w_np[0] for w_np, _ in parts], axis=1))
+    assert np.array_equal(z.cpu().numpy(), np.concatenate([w_np[2] for w_np, _ in parts], axis=1))
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, qkv.n), dtype=TORCH[dtype], device=device)
+    hm.packed_linear(y, x, qkv)
+    sep = [hm.packed_linear(torch.empty((m, w.n), dtype=TORCH[dtype], device=device), x, w) for _, w in parts]
+    torch.cuda.synchronize()
+    ref = torch.cat(sep, dim=1)
+    if m == 1 or m > 16:
+        assert torch.equal(y, ref)
+    wf = np.concatenate([oracle.weights_f64(*w_np, g, dtype) for w_np, _ in parts], axis=1)
+    assert_close(oracle, host_f64(y), x64 @ wf, dtype, f"QKV M={m}")
