@@ -7,16 +7,18 @@
 // multiplies it with activation fragments read from LDS. The weight rounding to fp16 / bf16 happens once per
 // weight, as in the reference GEMM (src/hipkernels/w4a16_gemm_packed.cu:491-497); accumulation is fp32.
 //
-// Workgroup = 4 waves side by side over a BM x 128 output tile; a wave owns all BM = 16 RBW rows of 2 strips
-// (32 columns), so each dequantized B operand feeds RBW MFMAs (8 at BM = 128: about two VALU instructions per
-// MFMA). The activation tile (BM x 128 per K tile) goes from memory straight into LDS (buffer_load ... lds, no
-// registers), double-buffered, its 16-byte chunks XOR-swizzled by row so that an MFMA operand read touches 16
-// distinct bank groups; one barrier per K tile.
+// Workgroup = WN waves side by side over a BM x (32 WN) output tile (4 waves over 64 x 128 or 128 x 128, or 8
+// waves over 128 x 256); a wave owns all BM = 16 RBW rows of 2 strips (32 columns), so each dequantized B
+// operand feeds RBW MFMAs (8 at BM = 128: about two VALU instructions per MFMA). The activation tile (BM x 128
+// per K tile) goes from memory straight into LDS (buffer_load ... lds, no registers) and serves all WN waves;
+// its 16-byte chunks are XOR-swizzled by row so that an MFMA operand read touches 16 distinct bank groups; one
+// barrier per K tile.
 //
 // Software pipeline: while the MFMAs of 32-K step mu run, the VALU builds the B operands of step mu + 1 (of the
 // next K tile at mu = 3) and the LDS delivers the activation fragments of step mu + 1; sched_group_barrier
-// interleaves one MFMA with two VALU instructions. The next K tile's weights and activations are requested at
-// the start of each K tile.
+// interleaves one MFMA with two VALU instructions. K tile kt + DEPTH - 1's weights and activations are requested
+// at the start of K tile kt (DEPTH 2, or 4 for the 64-row tiles, whose small grids expose each workgroup's own
+// latency).
 //
 // Tiles are dealt to XCDs in contiguous runs (workgroup i runs on XCD i % 8), row tile outermost, so the
 // workgroups resident on one XCD share activation rows in its L2 while the weights stream.

@@ -4,9 +4,9 @@
 // strips) over a contiguous run of the K tiles of its split; `wps` waves share a strip group's K range and add
 // their partial sums through LDS at the end. A workgroup holds `nu` strip groups over one K range (split), so
 // the activation chunk it stages in LDS once serves nu * S strips: for M > 1 that chunk is M times larger
-// than for one row, and sharing it is what keeps its L2 -> LDS traffic below the weight traffic. Splits only
-// bound the staged chunk (64 KiB); their fp32 partials are added by sum_splits, which applies SwiGLU when
-// fused.
+// than for one row, and sharing it is what keeps its L2 -> LDS traffic below the weight traffic. Splits bound
+// the staged chunk and, with several rows, widen narrow grids; their fp32 partials are added by sum_splits,
+// which applies SwiGLU when fused.
 //
 // Streaming. Each wave keeps a ring of KB steps (S strip tiles and their scale/zero records per step) in
 // flight: the tile of step i + KB is requested as soon as step i has consumed its registers, and each step
@@ -25,8 +25,9 @@
 // src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:242-253), applied to MFMA partial sums. One LDS read of an
 // A fragment feeds the MFMAs of all S strips.
 //
-// Output: plain y = round(sum), fused act = round(SiLU(gate) * up) with fp32 math and one rounding
-// (kernels/gpu/src/silu_mul.cu:10-30), or fp32 partials per split.
+// Output: plain y = round(sum) (or, accumulating, y = round(y + round(sum)): a residual add), fused
+// act = round(SiLU(gate) * up) with fp32 math and one rounding (kernels/gpu/src/silu_mul.cu:10-30), or fp32
+// partials per split. One row may stage RMSNorm(x) * w instead of x (the layer-boundary norm).
 #include "hm_device.hpp"
 #include "hm_internal.hpp"
 
