@@ -632,16 +632,12 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
         return 0;
     }
     const size_t act = static_cast<size_t>(round_up(max_m * f->inter * 2, 256));
-    // The largest partial buffer of any M up to max_m (GEMV splits for M <= 16, GEMM K splits above,
-    // which only occur while the output tiles do not fill the chip).
+    // The largest partial buffer of any M up to max_m: only the GEMV (M <= 16) splits K; the GEMM never does.
     size_t partial = 0;
-    for (int64_t m = 1; m <= max_m; ++m) {
+    for (int64_t m = 1; m <= std::min<int64_t>(max_m, kGemvMaxRows); ++m) {
         const size_t d = linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false);
         const size_t g = linear_workspace(f->gate_up.p, m, f->inter, f->hidden / 128, true);
         partial = std::max(partial, std::max(d, g));
-        if (m > kGemvMaxRows && d == 0 && g == 0 && m >= 4096) {
-            break; // at this size every tile configuration fills the chip without splits
-        }
     }
     return act + partial;
 }
