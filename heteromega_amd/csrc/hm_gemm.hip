@@ -79,7 +79,7 @@ __device__ __forceinline__ Deq<F16> make_deq(uint32_t rec, F16) {
 
 __device__ __forceinline__ Deq<BF16> make_deq(uint32_t rec, BF16) {
     const float s = bf16_bits_to_float(rec & 0xFFFFu);
-    return Deq<BF16>{s, -(128.0f + static_cast<float>((rec >> 16) & 0xFFu)) * s};
+    return Deq<BF16>{s, -static_cast<float>((rec >> 16) & 0xFFu) * s};
 }
 
 // B operand of one 32-K step from one strip dword: (q - z) * s in the activation type.
@@ -100,19 +100,27 @@ __device__ __forceinline__ uint4 dequant_operand(uint32_t w, const Deq<F16> &q, 
     return b;
 }
 
-// bf16: exact (q - z) * s in fp32, then one round to nearest even (v_cvt_pk_bf16_f32).
+// bf16: exact (q - z) * s in fp32 (q * s and z * s carry at most 12 significant bits, so one FMA of them is
+// exact), then one round to nearest even (v_cvt_pk_bf16_f32). The nibbles go to bytes with two masks (bytes of
+// w & 0x0F0F0F0F hold nibbles 0, 2, 4, 6; of (w >> 4) & 0x0F0F0F0F nibbles 1, 3, 5, 7) and each byte to fp32
+// with one v_cvt_f32_ubyte, as gfx950 has no packed bf16 arithmetic.
 __device__ __forceinline__ uint4 dequant_operand(uint32_t w, const Deq<BF16> &q, const MagicRegs &m) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    uint4 b;
-    uint32_t *o = reinterpret_cast<uint32_t *>(&b);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t v = ((w >> (4 * i)) & m.lo) | m.magic;
-        const f2 r = {__builtin_fmaf(__uint_as_float(v << 16), q.s, q.ds), __builtin_fmaf(__uint_as_float(v & 0xFFFF0000u), q.s, q.ds)};
-        o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, b2));
-    }
-    return b;
+    (void)m;
+    uint32_t e = w & 0x0F0F0F0Fu;        // nibbles 0, 2, 4, 6
+    uint32_t o = (w >> 4) & 0x0F0F0F0Fu; // nibbles 1, 3, 5, 7
+    // Opaque to the optimizer, which would otherwise fold the masks into per-byte shifts and masks instead of
+    // the byte-selecting conversions.
+    asm volatile("" : "+v"(e), "+v"(o));
+    auto pair = [&](uint32_t src, int b0) __attribute__((always_inline)) {
+        const float lo = static_cast<float>(static_cast<uint8_t>(src >> (8 * b0)));
+        const float hi = static_cast<float>(static_cast<uint8_t>(src >> (8 * (b0 + 2))));
+        const f2 r = {__builtin_fmaf(lo, q.s, q.ds), __builtin_fmaf(hi, q.s, q.ds)};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(r, b2));
+    };
+    // dword i holds K elements 2i, 2i + 1 (nibbles i and 4 + i)
+    return uint4{pair(e, 0), pair(o, 0), pair(e, 1), pair(o, 1)};
 }
 
 template <class T, int G, int NSW> struct BTile {
