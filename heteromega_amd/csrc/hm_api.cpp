@@ -172,13 +172,19 @@ hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, i
 // Workspace for any call of M rows over up to n columns (any column range within them) and kt_count K tiles.
 size_t linear_workspace(const hm::Planes &p, int64_t M, int64_t n, int64_t kt_count, bool fused) {
     if (M > kGemvMaxRows) {
+        // A narrower column range has a smaller grid and may split K further: the largest plan over every width
+        // (at most kGemmPartialMax). More K tiles never split less, so kt_count itself bounds the K ranges.
         hm::GemmCall c;
         c.w = p;
         c.m = M;
-        c.n = n;
         c.kt_count = kt_count;
         c.fused = fused;
-        return hm::plan_gemm(c).partial_bytes;
+        size_t need = 0;
+        for (int64_t w = fused ? 64 : 128; w <= n; w += fused ? 64 : 128) {
+            c.n = w;
+            need = std::max(need, hm::plan_gemm(c).partial_bytes);
+        }
+        return need;
     }
     hm::GemvCall c;
     c.w = p;
@@ -632,8 +638,9 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
         return 0;
     }
     const size_t act = static_cast<size_t>(round_up(max_m * f->inter * 2, 256));
-    // The largest partial buffer of any M up to max_m: only the GEMV (M <= 16) splits K; the GEMM never does.
-    size_t partial = 0;
+    // The largest partial buffer of any M up to max_m and any channel range: the GEMV's (M <= 16) and, above,
+    // the GEMM's small-grid K split, which never needs more than kGemmPartialMax.
+    size_t partial = max_m > kGemvMaxRows ? hm::kGemmPartialMax : 0;
     for (int64_t m = 1; m <= std::min<int64_t>(max_m, kGemvMaxRows); ++m) {
         const size_t d = linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false);
         const size_t g = linear_workspace(f->gate_up.p, m, f->inter, f->hidden / 128, true);

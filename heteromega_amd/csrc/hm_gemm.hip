@@ -26,8 +26,9 @@
 // D element i of lane l is row 4 (l / 16) + i, column l % 16. Fused (gate_up, strips alternating gate / up
 // per 16 channels): a wave's two strips are the gate and up columns of the same channels in the same lanes, so
 // the epilogue writes SiLU(gate) * up with fp32 math and one rounding (kernels/gpu/src/gemm_w4a16.cu:229-275
-// fuses the same way). The K range is never split, so every output element accumulates in the same order for
-// any M and tile shape.
+// fuses the same way). Every output element accumulates in the same order for any M and tile shape. Grids of
+// under 128 workgroups split the K range instead (blockIdx.y = split): each split writes fp32 partials and
+// sum_splits adds them in split order, SwiGLU when fused.
 #include "hm_device.hpp"
 #include "hm_internal.hpp"
 
@@ -179,11 +180,14 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     const int tm = lin / a.tiles_n;
     const int tn = lin - tm * a.tiles_n;
     const int row0 = tm * BM;
-    const int nkt = a.kt_count;
+    // K split (small grids only): this workgroup's K tiles [kt_lo, kt_lo + nkt) of the call.
+    const int split = static_cast<int>(blockIdx.y);
+    const int kt_lo = split * a.kt_per_split;
+    const int nkt = min(a.kt_per_split, a.kt_count - kt_lo);
 
     // Buffer resources with per-wave bases; per K tile only the scalar offset moves.
     const int sbase = tn * (BN / 16) + wave * NSW; // first strip of this wave within the call
-    const int64_t tile0 = static_cast<int64_t>(a.strip_begin + sbase) * a.kt_pitch + a.kt_begin;
+    const int64_t tile0 = static_cast<int64_t>(a.strip_begin + sbase) * a.kt_pitch + a.kt_begin + kt_lo;
     const uint32_t qstrip = static_cast<uint32_t>(a.kt_pitch) * 1024u;
     const uint32_t mstrip = static_cast<uint32_t>(a.kt_pitch) * 64u * GPT;
     const __amdgpu_buffer_rsrc_t qr = buffer_rsrc(reinterpret_cast<const uint8_t *>(a.quant) + tile0 * 1024, NSW * qstrip);
@@ -194,7 +198,8 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
         return; // never for a consistent plan (its last tile row starts below M); a guard against one that is not
     }
     // x column 0 is the call's first K (kt_begin), as for the GEMV.
-    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(reinterpret_cast<const uint8_t *>(a.x) + static_cast<int64_t>(row0) * a.ldx * 2,
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(reinterpret_cast<const uint8_t *>(a.x) + static_cast<int64_t>(row0) * a.ldx * 2 +
+                                                      static_cast<int64_t>(kt_lo) * 256,
                                                   static_cast<uint32_t>(rows_here - 1) * ldx2 + static_cast<uint32_t>(nkt) * 256u);
     // Transfer j of this wave fills LDS bytes [(wave * ADMA + j) KiB, +1 KiB): lane l -> slot p = 64 (wave ADMA + j) + l,
     // row p / 16, swizzled chunk p % 16 (so source chunk (p % 16) ^ (row % 16)). Rows past M read row M - 1.
@@ -354,6 +359,28 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
         }
     }
 
+    if (a.partial != nullptr) {
+        // K split: fp32 partials [split][m][ncols] (strip order, so a fused call's gate and up columns alternate
+        // per 16), added by sum_splits. Rows past M fall outside the buffer and are dropped.
+        const uint32_t ldp4 = static_cast<uint32_t>(a.ncols) * 4u;
+        const __amdgpu_buffer_rsrc_t pr =
+            buffer_rsrc(a.partial + (static_cast<int64_t>(split) * a.m + row0) * a.ncols, static_cast<uint32_t>(rows_here) * ldp4);
+        const uint32_t pcol = static_cast<uint32_t>(4 * h) * ldp4 + static_cast<uint32_t>(sbase * 16 + col) * 4u;
+#pragma unroll
+        for (int rb = 0; rb < RBW; ++rb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ro = static_cast<uint32_t>(rb * 16 + i) * ldp4;
+#pragma unroll
+                for (int s = 0; s < NSW; ++s) {
+                    // Element first: a bit cast of a vector element expression reads element 0.
+                    const float v = acc[rb][s][i];
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), pr, pcol + s * 64u, ro, 0);
+                }
+            }
+        }
+        return;
+    }
     // Epilogue through a buffer covering this tile's valid rows: stores of rows past M fall outside it and are
     // dropped by the buffer range check, so no per-row branch; row offsets are scalar.
     const uint32_t ldy2 = static_cast<uint32_t>(a.ldy) * 2u;
@@ -424,8 +451,8 @@ GemmPlan plan_gemm(const GemmCall &c) {
     // 128 x 256 tiles (8 waves, one workgroup per CU; each staged activation tile feeds twice the strips) where
     // their grid is one round of 160..256 workgroups or six and more rounds: measured 4-7% faster there, and
     // 2-34% slower for one to six partial rounds and for small grids, where the 4-wave tiles balance better.
-    // The K range is never split: every output element accumulates in the same order for any M and tile
-    // shape, so a row block computed alone gives the same bits as inside a larger call.
+    // All three accumulate every output element in the same order, so without a K split a row block computed
+    // alone gives the same bits as inside a larger call.
     p.cfg = rows128 * (cols / 128) >= 5 * kCUs / 8 ? 1 : 0;
     const int64_t wide = cols % 256 == 0 ? rows128 * (cols / 256) : 0;
     if (p.cfg == 1 && ((wide >= 5 * kCUs / 8 && wide <= kCUs) || wide >= 6 * kCUs)) {
@@ -445,6 +472,21 @@ GemmPlan plan_gemm(const GemmCall &c) {
     p.kt_per_split = c.kt_count;
     p.splits = 1;
     p.partial_bytes = 0;
+    // Grids of under 128 workgroups (a down projection at up to 128 rows) split K until about 256 workgroups,
+    // with at least 8 K tiles per split and fp32 partials within kGemmPartialMax; a row block's bits then
+    // depend on the call's grid (larger grids never split).
+    const int64_t wgs = p.tiles_m * p.tiles_n;
+    if (wgs < kCUs / 2 && c.kt_count >= 16 && !std::getenv("HM_GEMM_NOSPLIT")) {
+        int64_t splits = std::min<int64_t>((kCUs + wgs - 1) / wgs, c.kt_count / 8);
+        while (splits > 1 && static_cast<size_t>(splits) * c.m * cols * sizeof(float) > kGemmPartialMax) {
+            --splits;
+        }
+        if (splits > 1) {
+            p.kt_per_split = (c.kt_count + splits - 1) / splits;
+            p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
+            p.partial_bytes = static_cast<size_t>(p.splits) * c.m * cols * sizeof(float);
+        }
+    }
     return p;
 }
 

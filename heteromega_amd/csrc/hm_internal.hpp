@@ -86,8 +86,9 @@ struct GemmCall {
     bool fused = false;
     float *partial = nullptr; // split-K partials (GemmPlan::partial_bytes)
 };
-// Tile configuration (2: 128 x 256 tiles, 8 waves; 1: 128 x 128, 4 waves; 0: 64 x 128, 4 waves). The GEMM does
-// not split K (splits = 1, no partials); the fields keep the GEMV's plan shape.
+// Tile configuration (2: 128 x 256 tiles, 8 waves; 1: 128 x 128, 4 waves; 0: 64 x 128, 4 waves). The GEMM splits
+// K only for grids of under 128 workgroups, with fp32 partials of at most kGemmPartialMax bytes.
+constexpr size_t kGemmPartialMax = 16u << 20;
 struct GemmPlan {
     int cfg = 1;
     int64_t tiles_m = 0, tiles_n = 0;

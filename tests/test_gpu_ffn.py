@@ -65,6 +65,22 @@ def test_ffn_prefill_llama3_8b(oracle, hm, device, dtype, m, rows):
         assert torch.equal(y_part, y[128:384])
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("m", [40, 100])
+def test_ffn_gemm_k_split(oracle, hm, device, dtype, m):
+    # Small GEMM grids split K: hidden 2688 = 21 K tiles (the fused gate_up's 36 column tiles split 11 + 10,
+    # SwiGLU applied after the split sum), intermediate 2304 = 18 K tiles (the down's 21 column tiles split
+    # 9 + 9); M not a multiple of the 64-row tile. All rows against the oracle, and the bits equal a repeat call.
+    layer, _, wf = _layer(oracle, hm, device, 2688, 2304, 128, dtype, 4)
+    rng = np.random.default_rng(25 + m)
+    x64, x = make_x(oracle, rng, m, 2688, dtype, device)
+    y = layer.forward(x)
+    y2 = layer.forward(x)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, dtype), dtype, f"K-split FFN M={m}")
+    assert torch.equal(y, y2)
+
+
 def test_ffn_qwen14b_group64(oracle, hm, device):
     layer, _, wf = _layer(oracle, hm, device, 5120, 13824, 64, "fp16", 2)
     rng = np.random.default_rng(30)
