@@ -121,7 +121,7 @@ constexpr int64_t kGemvMaxRows = 16;
 
 hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t strip_begin,
                      int64_t n, int64_t kt_begin, int64_t kt_count, bool fused, void *workspace, size_t workspace_bytes,
-                     hipStream_t stream) {
+                     hipStream_t stream, bool accumulate = false) {
     if (M <= kGemvMaxRows) {
         hm::GemvCall c;
         c.w = p;
@@ -135,6 +135,7 @@ hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, i
         c.kt_begin = kt_begin;
         c.kt_count = kt_count;
         c.fused = fused;
+        c.accumulate = accumulate;
         const size_t need = hm::plan_gemv(c).partial_bytes;
         if (need > workspace_bytes) {
             return fail(HM_WORKSPACE_TOO_SMALL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
@@ -160,6 +161,7 @@ hm_status run_linear(const hm::Planes &p, void *y, int64_t ldy, const void *x, i
     c.kt_begin = kt_begin;
     c.kt_count = kt_count;
     c.fused = fused;
+    c.accumulate = accumulate;
     const size_t need = hm::plan_gemm(c).partial_bytes;
     if (need > workspace_bytes) {
         return fail(HM_WORKSPACE_TOO_SMALL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
@@ -496,6 +498,42 @@ hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, in
         return st;
     }
     return run_linear(w->p, y, ldy, x, ldx, M, col_begin / 16, n, 0, k / 128, false, workspace, workspace_bytes, as_stream(stream));
+}
+
+size_t hm_linear_k_split_workspace_bytes(const hm_weights *w0, const hm_weights *w1, int64_t M, int64_t k0, int64_t k1, int64_t n) {
+    if (w0 == nullptr || w1 == nullptr || M <= 0 || k0 <= 0 || k1 <= 0 || n <= 0) {
+        return 0;
+    }
+    // The two launches run one after the other on one stream and share the workspace.
+    return std::max(linear_workspace(w0->p, M, n, k0 / 128, false), linear_workspace(w1->p, M, n, k1 / 128, false));
+}
+
+hm_status hm_linear_k_split(const hm_weights *w0, const hm_weights *w1, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M,
+                            int64_t k0, int64_t k1, int64_t n, void *workspace, size_t workspace_bytes, void *stream) {
+    if (w0 == nullptr || w1 == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_linear_k_split: null weights");
+    }
+    if (w0->p.dtype != w1->p.dtype) {
+        return fail(HM_INVALID_ARGUMENT, "hm_linear_k_split: the two shares have different activation types");
+    }
+    if (M <= 0 || k0 <= 0 || k1 <= 0 || n <= 0 || k0 % 128 || k1 % 128 || n % 16 || k0 > w0->p.K || k1 > w1->p.K || n > w0->p.N ||
+        n > w1->p.N) {
+        return fail(HM_INVALID_ARGUMENT,
+                    "hm_linear_k_split: k0=%lld, k1=%lld (multiples of 128) and n=%lld (multiple of 16) must fit [%lld, %lld] and [%lld, %lld]",
+                    static_cast<long long>(k0), static_cast<long long>(k1), static_cast<long long>(n), static_cast<long long>(w0->p.K),
+                    static_cast<long long>(w0->p.N), static_cast<long long>(w1->p.K), static_cast<long long>(w1->p.N));
+    }
+    hm_status st = check_activation(x, ldx, k0 + k1, "hm_linear_k_split x");
+    if (st != HM_OK || (st = check_output(y, ldy, n, "hm_linear_k_split y")) != HM_OK) {
+        return st;
+    }
+    // Share 0 writes y = round(x[:, :k0] W0); share 1 adds in its epilogue: y = round(y + round(x[:, k0:] W1)).
+    const hipStream_t s = as_stream(stream);
+    if ((st = run_linear(w0->p, y, ldy, x, ldx, M, 0, n, 0, k0 / 128, false, workspace, workspace_bytes, s)) != HM_OK) {
+        return st;
+    }
+    const uint16_t *x1 = static_cast<const uint16_t *>(x) + k0;
+    return run_linear(w1->p, y, ldy, x1, ldx, M, 0, n, 0, k1 / 128, false, workspace, workspace_bytes, s, true);
 }
 
 hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden, int64_t inter, hm_dtype dtype,

@@ -53,6 +53,7 @@ struct GemmArgs {
     int m;
     int ncols; // 16 * strips of the call
     int tiles_m, tiles_n;
+    int accumulate; // plain output: y = round(y + round(sum)) instead of y = round(sum)
 };
 
 // Per (strip, group) dequantization constants, made once per K tile from the scale/zero record.
@@ -400,7 +401,11 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
             } else {
 #pragma unroll
                 for (int s = 0; s < NSW; ++s) {
-                    __builtin_amdgcn_raw_buffer_store_b16(T::from_float(acc[rb][s][i]), yr, ycol + s * 32u, ro, 0);
+                    uint16_t v = T::from_float(acc[rb][s][i]);
+                    if (a.accumulate) {
+                        v = T::from_float(T::to_float(__builtin_amdgcn_raw_buffer_load_b16(yr, ycol + s * 32u, ro, 0)) + T::to_float(v));
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b16(v, yr, ycol + s * 32u, ro, 0);
                 }
             }
         }
@@ -509,6 +514,7 @@ hipError_t launch_gemm(const GemmCall &c, hipStream_t stream) {
     a.ncols = static_cast<int>(c.fused ? 2 * c.n : c.n);
     a.tiles_m = static_cast<int>(p.tiles_m);
     a.tiles_n = static_cast<int>(p.tiles_n);
+    a.accumulate = c.accumulate && !c.fused ? 1 : 0;
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(p.splits));
     const int group = static_cast<int>(c.w.group);
     hipError_t e = c.w.dtype == 1 ? launch_t<F16>(a, group, c.fused, p.cfg, grid, stream)
@@ -516,7 +522,7 @@ hipError_t launch_gemm(const GemmCall &c, hipStream_t stream) {
     if (e != hipSuccess || p.splits == 1) {
         return e;
     }
-    return launch_sum_splits(c.partial, c.y, c.ldy, c.m, a.ncols, static_cast<int>(p.splits), c.fused, c.w.dtype, stream);
+    return launch_sum_splits(c.partial, c.y, c.ldy, c.m, a.ncols, static_cast<int>(p.splits), c.fused, c.w.dtype, stream, c.accumulate);
 }
 
 } // namespace hm

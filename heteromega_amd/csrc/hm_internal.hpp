@@ -85,6 +85,7 @@ struct GemmCall {
     int64_t kt_begin = 0, kt_count = 0;
     bool fused = false;
     float *partial = nullptr; // split-K partials (GemmPlan::partial_bytes)
+    bool accumulate = false;  // plain output: y = round(y + round(x W))
 };
 // Tile configuration (2: 128 x 256 tiles, 8 waves; 1: 128 x 128, 4 waves; 0: 64 x 128, 4 waves). The GEMM splits
 // K only for grids of under 128 workgroups, with fp32 partials of at most kGemmPartialMax bytes.

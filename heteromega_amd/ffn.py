@@ -255,6 +255,30 @@ def packed_linear(out, inp, w, k=None, n=None, col_begin=0, stream=None, workspa
     return out
 
 
+def packed_linear_k_split(out, inp, w0, w1, k0=None, k1=None, n=None, stream=None, workspace=None):
+    """K split over a pair of packed matrices (hetero_matmul_out_gemm_packed_K / hetero_matmul_out_gemv_packed_K,
+    hetero_compute.cpp:282-447, 633-805, GPU-only): out = round(round(inp[:, :k0] @ W0) + round(inp[:, k0:k0 + k1] @ W1)),
+    the reference's sum of the two shares' outputs. Both shares run on the GPU; the second adds into out."""
+    k0 = w0.k if k0 is None else k0
+    k1 = w1.k if k1 is None else k1
+    n = min(w0.n, w1.n) if n is None else n
+    if inp.dim() != 2 or inp.size(1) < k0 + k1 or inp.stride(1) != 1:
+        raise ValueError(f"packed_linear_k_split: input must be [M, >= {k0 + k1}] with unit column stride")
+    m = inp.size(0)
+    if out.dim() != 2 or out.size(0) != m or out.size(1) < n or out.stride(1) != 1:
+        raise ValueError(f"packed_linear_k_split: output must be [M, >= {n}]")
+    if w0.dtype != w1.dtype or inp.dtype != w0.dtype or out.dtype != w0.dtype:
+        raise ValueError(f"packed_linear_k_split: input, output and both shares must be {w0.dtype}")
+    lib = _lib.load()
+    need = lib.hm_linear_k_split_workspace_bytes(w0._h, w1._h, m, k0, k1, n)
+    if workspace is None:
+        workspace = _workspace(need, inp.device)
+    wp, wb = _aligned(workspace, need)
+    _call(lib.hm_linear_k_split(w0._h, w1._h, _ptr(out), out.stride(0), _ptr(inp), inp.stride(0), m, k0, k1, n, wp, wb,
+                                _stream(stream, inp.device)))
+    return out
+
+
 def gemv_w4a16(out, x, w, k=None, n=None, col_begin=0, stream=None):
     """M = 1 (heteromega::gemv_w4a16, gpu_ffn.hpp:99-103)."""
     if x.dim() != 2 or x.size(0) != 1:
@@ -557,6 +581,6 @@ class GpuFfnModel:
 
 __all__ = [
     "HMError", "kTileK", "kTileN", "kTileBytes", "padded_rows", "packed_bytes", "packed_tile_index", "pack_w4a16",
-    "awq_unpack_qweight", "awq_unpack_qzeros", "gptq_unpack_qweight", "gptq_unpack_qzeros", "RepackedMatrix", "packed_linear", "gemv_w4a16", "gemm_w4a16", "silu_mul",
+    "awq_unpack_qweight", "awq_unpack_qzeros", "gptq_unpack_qweight", "gptq_unpack_qzeros", "RepackedMatrix", "packed_linear", "packed_linear_k_split", "gemv_w4a16", "gemm_w4a16", "silu_mul",
     "rmsnorm", "residual_add2", "residual_rmsnorm", "FfnLayer", "FFNPartition", "ffn_partitioned", "ffn_row_split", "GpuFfnModel",
 ]

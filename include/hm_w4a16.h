@@ -153,6 +153,24 @@ hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, in
                     int64_t n, int64_t col_begin, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * K split of one projection over two packed matrices (the pre-saved K-split
+ * pair, W0 = rows [0, k0) and W1 = rows [k0, k0 + k1) of W):
+ *   y[M, n] = round(round(x[:, :k0] W0[:, :n]) + round(x[:, k0:k0+k1] W1[:, :n])).
+ * Replaces hetero_matmul_out_gemm_packed_K and hetero_matmul_out_gemv_packed_K
+ * (src/unified_llm_w4a16_hetero/hetero_compute.cpp:282-447 and 633-805), which
+ * give the K0 share to the NPU or, GPU-only, run both shares and sum their
+ * rounded outputs (output_2d.add_(temp_output), :437 and :800). Both shares run
+ * on the GPU here: share 0 writes y, share 1 adds into y in its epilogue, so no
+ * temporary output and no extra pass. k0, k1 multiples of 128, n of 16; the
+ * two matrices have the same activation type. M <= 16 uses the GEMV.
+ * ------------------------------------------------------------------------- */
+size_t hm_linear_k_split_workspace_bytes(const hm_weights *w0, const hm_weights *w1, int64_t M, int64_t k0, int64_t k1,
+                                         int64_t n);
+hm_status hm_linear_k_split(const hm_weights *w0, const hm_weights *w1, void *y, int64_t ldy, const void *x, int64_t ldx,
+                            int64_t M, int64_t k0, int64_t k1, int64_t n, void *workspace, size_t workspace_bytes,
+                            void *stream);
+
+/* ---------------------------------------------------------------------------
  * One SwiGLU FFN layer: y = (SiLU(x Wg) * (x Wu)) Wd over the channels
  * [ch_begin, ch_end) of the layer (the row/column partition: the GPU share of
  * the reference's channel split, kernels/gpu/src/gpu_ffn.cpp:77-119 and

@@ -193,3 +193,33 @@ def test_concat_qkv_equals_separate(oracle, hm, device, m):
         assert_close(oracle, host_f64(y), host_f64(ref), dtype, f"QKV one launch vs three M={m}")
     wf = np.concatenate([oracle.weights_f64(*w_np, g, dtype) for w_np, _ in parts], axis=1)
     assert_close(oracle, host_f64(y), x64 @ wf, dtype, f"QKV M={m}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("m", [1, 4, 16, 37, 512, 2048])
+@pytest.mark.parametrize("k0,k1", [(2560, 1536), (1536, 2560)])
+def test_linear_k_split_pair(oracle, hm, device, dtype, m, k0, k1):
+    # A K-split pair (rows [0, k0) and [k0, k0 + k1) of a [4096, 1024] projection) with both shares on the GPU
+    # (hetero_matmul_out_gem{v,m}_packed_K, GPU-only): bit for bit the reference's sum of the two shares' rounded
+    # outputs (out.add_(temp), here torch's add of two separate launches), and within tolerance of the oracle's
+    # round(round(a) + round(b)). The second share adds into the output in the GEMV epilogue (M = 1), in the
+    # split sums (M = 4, 16; the GEMM at M = 37 and 512 when its 20 K tiles split) and in the GEMM epilogue.
+    rng = np.random.default_rng(140 + m + k0)
+    n, g = 1024, 128
+    w0_np, w0 = _matrix(oracle, hm, rng, k0, n, g, dtype, device)
+    w1_np, w1 = _matrix(oracle, hm, rng, k1, n, g, dtype, device)
+    x64, x = make_x(oracle, rng, m, k0 + k1, dtype, device)
+    y = torch.full((m, n), float("nan"), dtype=TORCH[dtype], device=device)
+    hm.packed_linear_k_split(y, x, w0, w1)
+    y0 = hm.packed_linear(torch.empty((m, n), dtype=TORCH[dtype], device=device), x[:, :k0], w0)
+    y1 = hm.packed_linear(torch.empty((m, n), dtype=TORCH[dtype], device=device), x[:, k0:], w1)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0 + y1)
+    a = oracle.round_to((x64[:, :k0] @ oracle.weights_f64(*w0_np, g, dtype)).astype(np.float32), dtype).astype(np.float64)
+    b = oracle.round_to((x64[:, k0:] @ oracle.weights_f64(*w1_np, g, dtype)).astype(np.float32), dtype).astype(np.float64)
+    assert_close(oracle, host_f64(y), a + b, dtype, f"K split {k0}+{k1} M={m}")
+    if m == 1:
+        with pytest.raises(ValueError):
+            hm.packed_linear_k_split(y, x, w0, w1, n=1040)
+        with pytest.raises(ValueError):
+            hm.packed_linear_k_split(y, x, w0, w1, k0=k0 - 64)
