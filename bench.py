@@ -104,6 +104,49 @@ def qkv_bench(hm, torch, dev, h, g, sets=24):
     return out
 
 
+def ksplit_bench(hm, torch, dev, h, inter, g, sets=12):
+    """The down projection kept as a K-split pair (two [inter/2, h] matrices, both shares on the GPU, the second
+    adding into the output) against the same projection as one [inter, h] matrix."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    k0 = inter // 2
+
+    def mat(k):
+        q = torch.randint(0, 16, (k, h), dtype=torch.uint8, device=dev, generator=gen)
+        s = (torch.rand((k // g, h), device=dev, generator=gen) * 0.019 + 0.001).to(torch.float16)
+        z = torch.randint(0, 16, (k // g, h), dtype=torch.uint8, device=dev, generator=gen)
+        return hm.RepackedMatrix.from_logical(q, s, z, g, dtype=torch.float16)
+
+    pairs = [(mat(k0), mat(inter - k0)) for _ in range(sets)]
+    whole = [mat(inter) for _ in range(sets)]
+    torch.cuda.synchronize()
+    out = {}
+    for m, count in ((1, sets), (2048, 2)):
+        act = torch.randn((m, inter), device=dev).to(torch.float16)
+        y = torch.empty((m, h), device=dev, dtype=torch.float16)
+        ws = torch.empty(max(whole[0].workspace_bytes(m), 64 << 20) + 512, dtype=torch.uint8, device=dev)
+
+        def split():
+            for w0, w1 in pairs[:count]:
+                hm.packed_linear_k_split(y, act, w0, w1, workspace=ws)
+
+        def one():
+            for w in whole[:count]:
+                hm.packed_linear(y, act, w, workspace=ws)
+
+        t_split = time_graph(torch, graph_of(torch, split), 20, 0.3, 2) / count
+        t_one = time_graph(torch, graph_of(torch, one), 20, 0.3, 2) / count
+        if m == 1:
+            b = inter * h // 2 + (inter // g) * h * 3
+            out["decode_M1"] = {"us_k_split_pair": round(t_split * 1e6, 2), "us_one_matrix": round(t_one * 1e6, 2),
+                                "GB_s_k_split_pair": round(b / t_split / 1e9, 1)}
+        else:
+            f = 2.0 * m * h * inter
+            out[f"prefill_M{m}"] = {"us_k_split_pair": round(t_split * 1e6, 1), "us_one_matrix": round(t_one * 1e6, 1),
+                                    "TFLOP_s_k_split_pair": round(f / t_split / 1e12, 1)}
+    return out
+
+
 def graph_of(torch, fn):
     """Captures fn() (enqueueing on the current stream) into a HIP graph after one eager warm-up call."""
     s = torch.cuda.Stream()
@@ -400,6 +443,11 @@ def main():
         # launches against one launch on the concatenated matrix. 24 weight sets (300 MB) rotate at M = 1.
         extra["attention_qkv"] = qkv_bench(hm, torch, dev, H, G)
         log(f"attention QKV: {extra['attention_qkv']}")
+        # The down projection kept as a pre-saved K-split pair (split at I / 2, both shares on the GPU) against
+        # one matrix. 12 weight sets of each (700 MB) rotate at M = 1.
+        extra["down_k_split_pair"] = ksplit_bench(hm, torch, dev, H, I, G)
+        torch.cuda.empty_cache()
+        log(f"down projection as a K-split pair: {extra['down_k_split_pair']}")
 
         # Qwen2.5-14B FFN shape, group 64.
         qh, qi, qg = 5120, 13824, 64
