@@ -26,9 +26,10 @@
 // D element i of lane l is row 4 (l / 16) + i, column l % 16. Fused (gate_up, strips alternating gate / up
 // per 16 channels): a wave's two strips are the gate and up columns of the same channels in the same lanes, so
 // the epilogue writes SiLU(gate) * up with fp32 math and one rounding (kernels/gpu/src/gemm_w4a16.cu:229-275
-// fuses the same way). Every output element accumulates in the same order for any M and tile shape. Grids of
-// under 128 workgroups split the K range instead (blockIdx.y = split): each split writes fp32 partials and
-// sum_splits adds them in split order, SwiGLU when fused.
+// fuses the same way). Every output element accumulates in the same order for any M and tile shape. Small
+// grids (under 128 workgroups, or 4-wave grids under two workgroups per CU) split the K range instead
+// (blockIdx.y = split): each split writes fp32 partials and sum_splits adds them in split order, SwiGLU when
+// fused.
 #include "hm_device.hpp"
 #include "hm_internal.hpp"
 
@@ -477,12 +478,19 @@ GemmPlan plan_gemm(const GemmCall &c) {
     p.kt_per_split = c.kt_count;
     p.splits = 1;
     p.partial_bytes = 0;
-    // Grids of under 128 workgroups (a down projection at up to 128 rows) split K until about 256 workgroups,
-    // with at least 8 K tiles per split and fp32 partials within kGemmPartialMax; a row block's bits then
-    // depend on the call's grid (larger grids never split).
+    // Grids of under 128 workgroups (a down projection at up to 128 rows) split K toward 256 workgroups, and
+    // 4-wave grids of 128 to 511 workgroups (under two per CU: the down projection at 256..512 rows) toward 512,
+    // with at least 8 K tiles per split (24 in the larger grids, where the partials' traffic must stay small
+    // against each split's work) and fp32 partials within kGemmPartialMax. Measured on the Llama-3-8B layer,
+    // against no split: M = 256 / 384 / 512 126.5 / 172.6 / 203.1 -> 102.7 / 164.4 / 196.7 µs (fp16), the bf16 and
+    // Qwen2.5-14B shapes alike; aiming the small grids at 512 too was 2.7% slower at M = 128, and splitting
+    // 32 K tiles in two (a 1024-column projection at M = 2048) slower. A row block's bits then depend on whether
+    // its call splits (grids that do not split keep them).
     const int64_t wgs = p.tiles_m * p.tiles_n;
-    if (wgs < kCUs / 2 && c.kt_count >= 16 && !std::getenv("HM_GEMM_NOSPLIT")) {
-        int64_t splits = std::min<int64_t>((kCUs + wgs - 1) / wgs, c.kt_count / 8);
+    const bool small = wgs < kCUs / 2;
+    const int64_t aim = small ? kCUs : (p.cfg != 2 && wgs < 2 * kCUs ? 2 * kCUs : 0);
+    if (aim > 0 && c.kt_count >= 16 && !std::getenv("HM_GEMM_NOSPLIT")) {
+        int64_t splits = std::min<int64_t>((aim + wgs - 1) / wgs, c.kt_count / (small ? 8 : 24));
         while (splits > 1 && static_cast<size_t>(splits) * c.m * cols * sizeof(float) > kGemmPartialMax) {
             --splits;
         }

@@ -88,7 +88,8 @@ struct GemmCall {
     bool accumulate = false;  // plain output: y = round(y + round(x W))
 };
 // Tile configuration (2: 128 x 256 tiles, 8 waves; 1: 128 x 128, 4 waves; 0: 64 x 128, 4 waves). The GEMM splits
-// K only for grids of under 128 workgroups, with fp32 partials of at most kGemmPartialMax bytes.
+// K only for grids of under 128 workgroups and 4-wave grids of under 512, with fp32 partials of at most
+// kGemmPartialMax bytes.
 constexpr size_t kGemmPartialMax = 16u << 20;
 struct GemmPlan {
     int cfg = 1;

@@ -58,11 +58,16 @@ def test_ffn_prefill_llama3_8b(oracle, hm, device, dtype, m, rows):
     torch.cuda.synchronize()
     sel = np.arange(m) if rows is None else np.sort(rng.choice(m, rows, replace=False))
     assert_close(oracle, host_f64(y)[sel], _ffn_ref(oracle, x64[sel], wf, dtype), dtype, f"Llama-3-8B FFN prefill M={m}")
-    # rows are independent: a row block alone gives the same bits
-    if m >= 512:
+    # rows are independent: a row block alone gives the same bits where neither call splits K (M = 2048 and its
+    # 1024-row block), and equal within rounding where one does (M = 512: both down GEMMs split, differently)
+    if m == 2048:
+        y_part = layer.forward(x[512:1536].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(y_part, y[512:1536])
+    elif m >= 512:
         y_part = layer.forward(x[128:384].contiguous())
         torch.cuda.synchronize()
-        assert torch.equal(y_part, y[128:384])
+        assert_close(oracle, host_f64(y_part), host_f64(y[128:384]), dtype, f"row block M={m}")
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
@@ -126,14 +131,21 @@ def test_partition_channel_split_qwen(oracle, hm, device, m):
 
 
 def test_partition_row_split_is_exact(oracle, hm, device):
+    # Row split (hetero_compute.cpp:189-259) with no call splitting K: the unsplit layer's bits. A share small
+    # enough that its down GEMM splits K (256 of 1024 rows) equals it within rounding.
     layer, _, _ = _layer(oracle, hm, device, 5120, 13824, 64, "fp16", 2)
     rng = np.random.default_rng(50)
-    _, x = make_x(oracle, rng, 1024, 5120, "fp16", device)
+    _, x = make_x(oracle, rng, 2048, 5120, "fp16", device)
     full = layer.forward(x)
     y = torch.empty_like(full)
-    hm.ffn_row_split(layer, x, y, 256)  # GPU rows [0, 768), the other share [768, 1024)
+    hm.ffn_row_split(layer, x, y, 512)  # GPU rows [0, 1536), the other share [1536, 2048)
     torch.cuda.synchronize()
     assert torch.equal(y, full)
+    full = layer.forward(x[:1024])
+    y = torch.empty_like(full)
+    hm.ffn_row_split(layer, x[:1024], y, 256)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), host_f64(full), "fp16", "row split 768/256")
 
 
 @pytest.mark.parametrize("m", [1, 16, 128])
