@@ -464,11 +464,11 @@ GemmPlan plan_gemm(const GemmCall &c) {
     if (p.cfg == 1 && ((wide >= 5 * kCUs / 8 && wide <= kCUs) || wide >= 6 * kCUs)) {
         p.cfg = 2;
     }
-    if (const char *v = std::getenv("HM_GEMM_CFG")) { // tuning override
-        const int cfg = std::atoi(v);
-        if (cfg >= 0 && cfg <= 2 && (cfg < 2 || cols % 256 == 0)) {
-            p.cfg = cfg;
-        }
+    // Tuning overrides, read once per process (the workspace query plans every column width).
+    static const int env_cfg = std::getenv("HM_GEMM_CFG") != nullptr ? std::atoi(std::getenv("HM_GEMM_CFG")) : -1;
+    static const bool env_nosplit = std::getenv("HM_GEMM_NOSPLIT") != nullptr;
+    if (env_cfg >= 0 && env_cfg <= 2 && (env_cfg < 2 || cols % 256 == 0)) {
+        p.cfg = env_cfg;
     }
     // Tile shape of each configuration; launch_g instantiates the kernel with the same shape.
     const int64_t bm = p.cfg >= 1 ? 128 : 64;
@@ -489,7 +489,7 @@ GemmPlan plan_gemm(const GemmCall &c) {
     const int64_t wgs = p.tiles_m * p.tiles_n;
     const bool small = wgs < kCUs / 2;
     const int64_t aim = small ? kCUs : (p.cfg != 2 && wgs < 2 * kCUs ? 2 * kCUs : 0);
-    if (aim > 0 && c.kt_count >= 16 && !std::getenv("HM_GEMM_NOSPLIT")) {
+    if (aim > 0 && c.kt_count >= 16 && !env_nosplit) {
         int64_t splits = std::min<int64_t>((aim + wgs - 1) / wgs, c.kt_count / (small ? 8 : 24));
         while (splits > 1 && static_cast<size_t>(splits) * c.m * cols * sizeof(float) > kGemmPartialMax) {
             --splits;
