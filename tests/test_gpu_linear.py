@@ -224,3 +224,28 @@ def test_linear_k_split_pair(oracle, hm, device, dtype, m, k0, k1):
             hm.packed_linear_k_split(y, x, w0, w1, n=1040)
         with pytest.raises(ValueError):
             hm.packed_linear_k_split(y, x, w0, w1, k0=k0 - 64)
+
+
+@pytest.mark.parametrize("m,k,n,col,g,dtype", [
+    (17, 2048, 1024, 0, 128, "fp16"),     # 8 workgroups: K split in 2 (8 tiles each)
+    (100, 4096, 512, 0, 64, "bf16"),      # group 64, 8 workgroups: K split in 4
+    (130, 2560, 768, 0, 32, "fp16"),      # group 32, 18 workgroups: 20 K tiles split 10 + 10
+    (257, 3072, 1280, 0, 64, "bf16"),     # 50 workgroups: 24 K tiles split in 3
+    (300, 6144, 4096, 0, 128, "fp16"),    # 160 four-wave workgroups: split in 2 toward two per CU
+    (300, 6144, 4096, 0, 128, "bf16"),
+    (64, 1024, 128, 0, 128, "fp16"),      # 8 K tiles: too few to split
+    (1000, 1024, 2048, 0, 128, "fp16"),   # 256 four-wave workgroups, 8 K tiles: no split
+    (33, 2048, 384, 256, 128, "fp16"),    # a column range on the GEMM path, split in 2
+    (9, 2048, 96, 512, 128, "bf16"),      # a column range on the GEMV path
+])
+def test_linear_planner_shapes(oracle, hm, device, m, k, n, col, g, dtype):
+    # Launch plans across the GEMM's K-split rules (small grids toward 256 workgroups, 4-wave grids toward two
+    # per CU, ragged splits, group 32 / 64, column ranges) against the oracle on every row.
+    rng = np.random.default_rng(160 + m + k // 128)
+    w_np, w = _matrix(oracle, hm, rng, k, col + n + 128, g, dtype, device)
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=TORCH[dtype], device=device)
+    hm.packed_linear(y, x, w, n=n, col_begin=col)
+    torch.cuda.synchronize()
+    ref = x64 @ oracle.weights_f64(*w_np, g, dtype)[:, col:col + n]
+    assert_close(oracle, host_f64(y), ref, dtype, f"linear M={m} K={k} cols [{col}, {col + n}) g={g}")
