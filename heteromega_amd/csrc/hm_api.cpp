@@ -504,8 +504,10 @@ size_t hm_linear_k_split_workspace_bytes(const hm_weights *w0, const hm_weights 
     if (w0 == nullptr || w1 == nullptr || M <= 0 || k0 <= 0 || k1 <= 0 || n <= 0) {
         return 0;
     }
-    // The two launches run one after the other on one stream and share the workspace.
-    return std::max(linear_workspace(w0->p, M, n, k0 / 128, false), linear_workspace(w1->p, M, n, k1 / 128, false));
+    // The two launches run one after the other on one stream and share the workspace; at one row the pair may
+    // run as one launch with a partial sum per share.
+    const size_t pair = M == 1 ? 2 * static_cast<size_t>(n) * sizeof(float) : 0;
+    return std::max({linear_workspace(w0->p, M, n, k0 / 128, false), linear_workspace(w1->p, M, n, k1 / 128, false), pair});
 }
 
 hm_status hm_linear_k_split(const hm_weights *w0, const hm_weights *w1, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M,
@@ -527,8 +529,31 @@ hm_status hm_linear_k_split(const hm_weights *w0, const hm_weights *w1, void *y,
     if (st != HM_OK || (st = check_output(y, ldy, n, "hm_linear_k_split y")) != HM_OK) {
         return st;
     }
-    // Share 0 writes y = round(x[:, :k0] W0); share 1 adds in its epilogue: y = round(y + round(x[:, k0:] W1)).
     const hipStream_t s = as_stream(stream);
+    // One row: both shares in one GEMV launch (split s runs share s), their rounded sums added by the split sum.
+    if (M == 1) {
+        hm::GemvCall c0, c1;
+        c0.w = w0->p;
+        c1.w = w1->p;
+        c0.x = static_cast<const uint16_t *>(x);
+        c1.x = c0.x + k0;
+        c0.ldx = c1.ldx = ldx;
+        c0.y = c1.y = static_cast<uint16_t *>(y);
+        c0.ldy = c1.ldy = ldy;
+        c0.n = c1.n = n;
+        c0.kt_count = k0 / 128;
+        c1.kt_count = k1 / 128;
+        if (hm::gemv_pair_supported(c0, c1)) {
+            const size_t need = hm::gemv_pair_partial_bytes(c0);
+            if (need > workspace_bytes) {
+                return fail(HM_WORKSPACE_TOO_SMALL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+            }
+            c0.partial = static_cast<float *>(workspace);
+            const hipError_t e = hm::launch_gemv_pair(c0, c1, k0, s);
+            return e == hipSuccess ? HM_OK : hip_fail(e, "gemv pair launch");
+        }
+    }
+    // Share 0 writes y = round(x[:, :k0] W0); share 1 adds in its epilogue: y = round(y + round(x[:, k0:] W1)).
     if ((st = run_linear(w0->p, y, ldy, x, ldx, M, 0, n, 0, k0 / 128, false, workspace, workspace_bytes, s)) != HM_OK) {
         return st;
     }

@@ -64,6 +64,11 @@ struct GemvArgs {
     const uint16_t *norm_w;
     float norm_eps;
     bool accumulate; // plain output: y = round(y + round(sum)) (a residual add) instead of y = round(sum)
+    // K-split pair (one row, two splits): split 1 reads a second matrix over x[k0, k0 + 128 kt_count2).
+    const uint4 *quant2;
+    const uint32_t *meta2;
+    int kt_pitch2, kt_count2;
+    int k0;
 };
 
 // v plus v of another lane of the same row of 16 (DPP control CTRL).
@@ -113,11 +118,12 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int h = lane >> 4;
 
     const int split = blockIdx.y;
-    const int kt0 = a.kt_begin + split * a.kt_per_split;
-    const int nkt = min(a.kt_per_split, a.kt_begin + a.kt_count - kt0);
+    const bool second = a.quant2 != nullptr && split == 1; // the pair's second matrix
+    const int kt0 = second ? 0 : a.kt_begin + split * a.kt_per_split;
+    const int nkt = second ? a.kt_count2 : min(a.kt_per_split, a.kt_begin + a.kt_count - kt0);
     const int kc = nkt * 128; // K values of this split
     const int kg = kc / G;    // groups of this split
-    const int64_t xk0 = static_cast<int64_t>(kt0 - a.kt_begin) * 128;
+    const int64_t xk0 = second ? static_cast<int64_t>(a.k0) : static_cast<int64_t>(kt0 - a.kt_begin) * 128;
 
     // Row strides padded by 16 bytes (x) and 8 bytes (sums) so that lanes reading different rows of one MFMA
     // operand or fold hit different LDS banks.
@@ -138,9 +144,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const uint32_t *mp[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-        const int64_t tile0 = static_cast<int64_t>(strip0 + s) * a.kt_pitch + kt0;
-        qp[s] = a.quant + tile0 * 64;
-        mp[s] = a.meta + tile0 * 16 * GPT;
+        const int64_t tile0 = static_cast<int64_t>(strip0 + s) * (second ? a.kt_pitch2 : a.kt_pitch) + kt0;
+        qp[s] = (second ? a.quant2 : a.quant) + tile0 * 64;
+        mp[s] = (second ? a.meta2 : a.meta) + tile0 * 16 * GPT;
     }
     const int tpw = (nkt + a.wps - 1) / a.wps;
     const int tb = wi * tpw;
@@ -479,7 +485,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 // output is SiLU(gate) * up per channel (ncols / 2 channels).
 template <class T, bool FUSED>
 __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ partial, uint16_t *__restrict__ y, int64_t ldy, int m,
-                                                  int ncols, int splits, bool accumulate) {
+                                                  int ncols, int splits, bool accumulate, bool pairwise) {
     const int nout = FUSED ? ncols / 2 : ncols;
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= static_cast<int64_t>(m) * nout) {
@@ -488,6 +494,16 @@ __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ part
     const int row = static_cast<int>(idx / nout);
     const int c = static_cast<int>(idx - static_cast<int64_t>(row) * nout);
     const int cg = FUSED ? (c >> 4) * 32 + (c & 15) : c; // gate (or plain) column
+    if (!FUSED && pairwise) {
+        // A K-split pair: each share's sum is rounded, then they are added with one more rounding, as
+        // round(round(x0 W0) + round(x1 W1)) (plain outputs only).
+        float v = T::to_float(T::from_float(partial[static_cast<int64_t>(row) * ncols + cg]));
+        for (int s = 1; s < splits; ++s) {
+            v = T::to_float(T::from_float(v + T::to_float(T::from_float(partial[(static_cast<int64_t>(s) * m + row) * ncols + cg]))));
+        }
+        y[row * ldy + c] = T::from_float(v);
+        return;
+    }
     // Eight splits' loads are in flight at once (a load per split and a wait per add would put the splits'
     // memory latencies in series); the sums still run in split order.
     constexpr int kBatch = 8;
@@ -667,12 +683,10 @@ size_t gemv_partial_bound(const GemvCall &c) {
     return std::max(p.partial_bytes, narrow);
 }
 
-hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
-    const GemvPlan p = plan_gemv(c);
-    if (p.waves != 4 && p.waves != 8 && p.waves != 16) {
-        return hipErrorInvalidConfiguration;
-    }
-    GemvArgs a;
+namespace {
+
+GemvArgs make_args(const GemvCall &c, const GemvPlan &p) {
+    GemvArgs a{};
     a.quant = reinterpret_cast<const uint4 *>(c.w.quant);
     a.meta = c.w.meta;
     a.x = c.x;
@@ -693,32 +707,74 @@ hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
     a.norm_w = c.norm_w;
     a.norm_eps = c.norm_eps;
     a.accumulate = c.accumulate;
-    const dim3 grid(static_cast<unsigned>((p.groups + p.nu - 1) / p.nu), static_cast<unsigned>(p.splits));
+    return a;
+}
+
+hipError_t launch_args(const GemvArgs &a, const GemvCall &c, const GemvPlan &p, unsigned splits, hipStream_t stream) {
+    if (p.waves != 4 && p.waves != 8 && p.waves != 16) {
+        return hipErrorInvalidConfiguration;
+    }
+    const dim3 grid(static_cast<unsigned>((p.groups + p.nu - 1) / p.nu), splits);
     const int group = static_cast<int>(c.w.group);
-    hipError_t e = c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream)
-                                  : launch_dtype<BF16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream);
+    return c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream)
+                          : launch_dtype<BF16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream);
+}
+
+} // namespace
+
+hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
+    const GemvPlan p = plan_gemv(c);
+    const GemvArgs a = make_args(c, p);
+    const hipError_t e = launch_args(a, c, p, static_cast<unsigned>(p.splits), stream);
     if (e != hipSuccess || p.splits == 1) {
         return e;
     }
     return launch_sum_splits(c.partial, c.y, c.ldy, c.m, a.ncols, static_cast<int>(p.splits), c.fused, c.w.dtype, stream, c.accumulate);
 }
 
+bool gemv_pair_supported(const GemvCall &c0, const GemvCall &c1) {
+    return c0.m == 1 && c1.m == 1 && !c0.fused && !c1.fused && c0.n == c1.n && c0.strip_begin == c1.strip_begin &&
+           c0.w.group == c1.w.group && c0.w.dtype == c1.w.dtype && c0.norm_w == nullptr && c1.norm_w == nullptr &&
+           !c0.accumulate && !c1.accumulate && c1.kt_begin == 0 && plan_gemv(c0).splits == 1 && plan_gemv(c1).splits == 1;
+}
+
+size_t gemv_pair_partial_bytes(const GemvCall &c0) { return 2 * static_cast<size_t>(c0.m) * static_cast<size_t>(c0.n) * sizeof(float); }
+
+hipError_t launch_gemv_pair(const GemvCall &c0, const GemvCall &c1, int64_t k0, hipStream_t stream) {
+    // The launch shape of the longer share (its LDS covers the shorter one's staging); split s runs share s.
+    GemvPlan p = plan_gemv(c0.kt_count >= c1.kt_count ? c0 : c1);
+    p.splits = 2;
+    GemvArgs a = make_args(c0, p);
+    a.partial = c0.partial;
+    a.kt_per_split = static_cast<int>(c0.kt_count);
+    a.quant2 = reinterpret_cast<const uint4 *>(c1.w.quant);
+    a.meta2 = c1.w.meta;
+    a.kt_pitch2 = static_cast<int>(c1.w.kt_pitch());
+    a.kt_count2 = static_cast<int>(c1.kt_count);
+    a.k0 = static_cast<int>(k0);
+    const hipError_t e = launch_args(a, c0, p, 2u, stream);
+    if (e != hipSuccess) {
+        return e;
+    }
+    return launch_sum_splits(c0.partial, c0.y, c0.ldy, c0.m, a.ncols, 2, false, c0.w.dtype, stream, false, true);
+}
+
 hipError_t launch_sum_splits(const float *partial, uint16_t *y, int64_t ldy, int64_t m, int ncols, int splits, bool fused,
-                             int dtype, hipStream_t stream, bool accumulate) {
+                             int dtype, hipStream_t stream, bool accumulate, bool pairwise) {
     const int64_t total = m * (fused ? ncols / 2 : ncols);
     const dim3 blocks(static_cast<unsigned>((total + 255) / 256));
     const int mi = static_cast<int>(m);
     if (dtype == 1) {
         if (fused) {
-            hipLaunchKernelGGL((sum_splits<F16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
+            hipLaunchKernelGGL((sum_splits<F16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate, pairwise);
         } else {
-            hipLaunchKernelGGL((sum_splits<F16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
+            hipLaunchKernelGGL((sum_splits<F16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate, pairwise);
         }
     } else {
         if (fused) {
-            hipLaunchKernelGGL((sum_splits<BF16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
+            hipLaunchKernelGGL((sum_splits<BF16, true>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate, pairwise);
         } else {
-            hipLaunchKernelGGL((sum_splits<BF16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate);
+            hipLaunchKernelGGL((sum_splits<BF16, false>), blocks, dim3(256), 0, stream, partial, y, ldy, mi, ncols, splits, accumulate, pairwise);
         }
     }
     return hipGetLastError();

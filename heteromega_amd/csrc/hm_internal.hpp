@@ -71,6 +71,11 @@ GemvPlan plan_gemv(const GemvCall &c);
 // The largest partial buffer of a call like c over any range of c's columns (narrower ranges split K more).
 size_t gemv_partial_bound(const GemvCall &c);
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream);
+// A K-split pair at one row in one launch: split 0 runs c0, split 1 runs c1 (x advanced by k0 elements), and the
+// split sum forms round(round(c0) + round(c1)) into c0.y. c0.partial holds gemv_pair_partial_bytes(c0).
+bool gemv_pair_supported(const GemvCall &c0, const GemvCall &c1);
+size_t gemv_pair_partial_bytes(const GemvCall &c0);
+hipError_t launch_gemv_pair(const GemvCall &c0, const GemvCall &c1, int64_t k0, hipStream_t stream);
 
 // Prefill GEMM (MFMA 32x32x16) with the same operand conventions; fused writes SiLU(gate) * up.
 struct GemmCall {
@@ -102,8 +107,9 @@ hipError_t launch_gemm(const GemmCall &c, hipStream_t stream);
 
 // Adds split-K partials [splits][m][ncols] into y [m, ncols] (or, fused, y [m, ncols / 2] = SiLU(gate) * up
 // with gate and up alternating per 16 columns).
+// pairwise (plain only): each split's sum rounded, then added in split order with one rounding per add.
 hipError_t launch_sum_splits(const float *partial, uint16_t *y, int64_t ldy, int64_t m, int ncols, int splits, bool fused,
-                             int dtype, hipStream_t stream, bool accumulate = false);
+                             int dtype, hipStream_t stream, bool accumulate = false, bool pairwise = false);
 
 hipError_t launch_silu_mul(const uint16_t *gate_up, int64_t ld_in, uint16_t *act, int64_t ld_out, int64_t rows, int64_t n,
                            bool interleaved, int dtype, hipStream_t stream);

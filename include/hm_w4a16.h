@@ -160,9 +160,11 @@ hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, in
  * (src/unified_llm_w4a16_hetero/hetero_compute.cpp:282-447 and 633-805), which
  * give the K0 share to the NPU or, GPU-only, run both shares and sum their
  * rounded outputs (output_2d.add_(temp_output), :437 and :800). Both shares run
- * on the GPU here: share 0 writes y, share 1 adds into y in its epilogue, so no
- * temporary output and no extra pass. k0, k1 multiples of 128, n of 16; the
- * two matrices have the same activation type. M <= 16 uses the GEMV.
+ * on the GPU here. At M = 1 (same group size) both shares run in one GEMV
+ * launch, each writing an fp32 partial that the split sum rounds and adds;
+ * otherwise share 0 writes y and share 1 adds into y in its epilogue (no
+ * temporary output, no extra pass). k0, k1 multiples of 128, n of 16; the two
+ * matrices have the same activation type. M <= 16 uses the GEMV.
  * ------------------------------------------------------------------------- */
 size_t hm_linear_k_split_workspace_bytes(const hm_weights *w0, const hm_weights *w1, int64_t M, int64_t k0, int64_t k1,
                                          int64_t n);
