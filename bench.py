@@ -418,6 +418,18 @@ def main():
     torch.cuda.empty_cache()
 
     if not args.quick:
+        # bf16 activations and scales (the reference operator's type): the same decode and prefill workloads.
+        bl = make_layers(hm, torch, dev, H, I, G, args.sets, dtype=torch.bfloat16, seed=7)
+        s1, _, _ = decode_bench(hm, torch, dev, bl, 1, H, args.steps, args.warmup)
+        s2 = prefill_bench(hm, torch, dev, bl, 2048, H, max(4, args.steps // 24), 2)
+        b1, f2 = ffn_bytes(1, H, I, G), ffn_flops(2048, H, I)
+        extra["bf16_activations"] = {"decode_M1_us": round(s1 * 1e6, 2), "decode_M1_GB_s": round(b1 / s1 / 1e9, 1),
+                                     "prefill_M2048_TFLOP_s": round(f2 / s2 / 1e12, 1),
+                                     "prefill_M2048_frac_mfma": round(f2 / s2 / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+        log(f"bf16: {extra['bf16_activations']}")
+        del bl
+        torch.cuda.empty_cache()
+
         # 32 distinct layers, RMSNorm (eps 1e-5) + residual between layers, decode M = 1.
         stack = make_layers(hm, torch, dev, H, I, G, 32, seed=1)
         # Each layer is one pre-norm FFN block, x += FFN(RMSNorm(x)): two launches per layer (the norm runs in
