@@ -195,23 +195,25 @@ def event_time_graph(torch, g, replays):
 def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0):
     """Seconds per decode step (one FFN layer pass): exactly `steps` steps timed, `warmup` untimed before.
 
-    The steps cycle through the weight sets; one graph replay runs one step per set, and a second graph holds
-    the remainder when `steps` is not a multiple of the set count."""
+    The steps cycle through the weight sets. One graph replay runs about 48 steps (whole rounds over the sets),
+    as a decoder replays a model's layers per token, so the gap between graph replays is not charged to every
+    few layers; a second graph holds the remainder when `steps` is not a multiple of that."""
     x = torch.randn((m, h), device=dev).to(layers[0].dtype)
     y = torch.empty_like(x)
     ws = layers[0].workspace(m)
     sets = len(layers)
+    per_graph = sets * max(1, min(48 // sets, steps // sets))
 
     def run(count):
         def fn():
-            for L in layers[:count]:
-                L.forward(x, y, workspace=ws)
+            for i in range(count):
+                layers[i % sets].forward(x, y, workspace=ws)
         return fn
 
-    g = graph_of(torch, run(sets))
-    rest = steps % sets
+    g = graph_of(torch, run(per_graph))
+    rest = steps % per_graph
     g_rest = graph_of(torch, run(rest)) if rest else None
-    for _ in range(max(0, warmup) // sets + 1):
+    for _ in range(max(0, warmup) // per_graph + 1):
         g.replay()
     torch.cuda.synchronize()
     t_end = time.perf_counter() + warm_seconds
@@ -219,7 +221,7 @@ def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0):
         g.replay()
         torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps // sets):
+    for _ in range(steps // per_graph):
         g.replay()
     if g_rest is not None:
         g_rest.replay()
@@ -387,13 +389,16 @@ def main():
     x1 = keep[0]
     acts = torch.empty((1, I), dtype=torch.float16, device=dev)
 
+    rounds = max(1, 48 // args.sets) # launches per replay as in the decode steps above
+
     def run_gate_up():
-        for L in layers:
-            L.gate_up(x1, acts)
+        for _ in range(rounds):
+            for L in layers:
+                L.gate_up(x1, acts)
 
     g_gu = graph_of(torch, run_gate_up)
-    reps = max(4, args.steps // args.sets)
-    gu_sec = event_time_graph(torch, g_gu, reps) / args.sets
+    reps = max(4, args.steps // (args.sets * rounds))
+    gu_sec = event_time_graph(torch, g_gu, reps) / (args.sets * rounds)
     gu_bytes = 2 * (H * I // 2 + (H * I // G) * 3) + H * 2 + I * 2
     achieved = gu_bytes / gu_sec / 1e9
     out["roofline"] = {"kernel": "gemv_kernel<F16, 1, 128, 2, true, 256> (fused gate_up + SwiGLU, M=1)", "bound": "hbm",
