@@ -376,7 +376,8 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
 
     if (a.partial != nullptr) {
         // K split: fp32 partials [split][m][ncols] (strip order, so a fused call's gate and up columns alternate
-        // per 16), added by sum_splits. Rows past M fall outside the buffer and are dropped.
+        // per 16), added by sum_splits. Rows past M fall outside the buffer and are dropped: the row offset is
+        // part of the vector offset, which the buffer range check covers (the scalar offset is not checked).
         const uint32_t ldp4 = static_cast<uint32_t>(a.ncols) * 4u;
         const __amdgpu_buffer_rsrc_t pr =
             buffer_rsrc(a.partial + (static_cast<int64_t>(split) * a.m + row0) * a.ncols, static_cast<uint32_t>(rows_here) * ldp4);
@@ -390,14 +391,15 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
                 for (int s = 0; s < NSW; ++s) {
                     // Element first: a bit cast of a vector element expression reads element 0.
                     const float v = acc[rb][s][i];
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), pr, pcol + s * 64u, ro, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), pr, pcol + ro + s * 64u, 0, 0);
                 }
             }
         }
         return;
     }
     // Epilogue through a buffer covering this tile's valid rows: stores of rows past M fall outside it and are
-    // dropped by the buffer range check, so no per-row branch; row offsets are scalar.
+    // dropped by the buffer range check, so no per-row branch. The row offset goes into the vector offset: the
+    // range check covers the vector and instruction offsets, not the scalar offset.
     const uint32_t ldy2 = static_cast<uint32_t>(a.ldy) * 2u;
     const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(a.y + static_cast<int64_t>(row0) * a.ldy, static_cast<uint32_t>(rows_here) * ldy2);
     const uint32_t ycol = static_cast<uint32_t>(4 * h) * ldy2 + static_cast<uint32_t>(FUSED ? sbase / 2 * 16 + col : sbase * 16 + col) * 2u;
@@ -410,16 +412,16 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
                 for (int s = 0; s < NSW; s += 2) {
                     const uint16_t v = T::from_float(silu(acc[rb][s][i]) * acc[rb][s + 1][i]);
-                    __builtin_amdgcn_raw_buffer_store_b16(v, yr, ycol + (s / 2) * 32u, ro, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16(v, yr, ycol + ro + (s / 2) * 32u, 0, 0);
                 }
             } else {
 #pragma unroll
                 for (int s = 0; s < NSW; ++s) {
                     uint16_t v = T::from_float(acc[rb][s][i]);
                     if (a.accumulate) {
-                        v = T::from_float(T::to_float(__builtin_amdgcn_raw_buffer_load_b16(yr, ycol + s * 32u, ro, 0)) + T::to_float(v));
+                        v = T::from_float(T::to_float(__builtin_amdgcn_raw_buffer_load_b16(yr, ycol + ro + s * 32u, 0, 0)) + T::to_float(v));
                     }
-                    __builtin_amdgcn_raw_buffer_store_b16(v, yr, ycol + s * 32u, ro, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16(v, yr, ycol + ro + s * 32u, 0, 0);
                 }
             }
         }
