@@ -74,6 +74,7 @@ _SIGNATURES = {
     "hm_ffn_destroy": (ctypes.c_int, [P]),
     "hm_ffn_workspace_bytes": (SZ, [P, I64]),
     "hm_ffn_forward": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I64, P, SZ, P]),
+    "hm_ffn_forward_static": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I64, P]),
     "hm_ffn_block_workspace_bytes": (SZ, [P, I64]),
     "hm_ffn_block_forward": (ctypes.c_int, [P, P, I64, P, ctypes.c_float, I64, P, SZ, P]),
     "hm_ffn_gate_up": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I64, P, SZ, P]),

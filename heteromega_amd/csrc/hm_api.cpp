@@ -29,13 +29,18 @@ namespace {
 
 thread_local std::string g_error;
 
-hm_status fail(hm_status s, const char *fmt, ...) {
+hm_status vfail(hm_status s, const char *fmt, va_list ap) {
     char buf[512];
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    g_error = buf;
+    return s;
+}
+
+hm_status fail(hm_status s, const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    vfail(s, fmt, ap);
     va_end(ap);
-    g_error = buf;
     return s;
 }
 
@@ -227,6 +232,14 @@ hm_status check_channels(const hm_ffn *f, int64_t b, int64_t e) {
 }
 
 } // namespace
+
+hm_status hm::set_error(hm_status s, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vfail(s, fmt, ap);
+    va_end(ap);
+    return s;
+}
 
 extern "C" {
 

@@ -1,6 +1,8 @@
 // Host-side declarations shared by the C ABI (hm_api.cpp) and the kernel files.
 #pragma once
 
+#include "../../include/hm_w4a16.h"
+
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -8,6 +10,9 @@
 #include <string>
 
 namespace hm {
+
+// Records the message of a failed C ABI call for hm_last_error() on this thread and returns s.
+hm_status set_error(hm_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 
 // Device planes of one repacked matrix (layout: hm_device.hpp).
 struct Planes {

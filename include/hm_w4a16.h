@@ -215,6 +215,18 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m);
 hm_status hm_ffn_forward(const hm_ffn *f, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M,
                          int64_t ch_begin, int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream);
 
+/* hm_ffn_forward without a workspace argument: the scratch (SwiGLU activation and split partials) is a static
+ * device array of HM_STATIC_SCRATCH_BYTES that the library holds on each GPU it runs on until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc); the call itself allocates nothing. The scratch must hold
+ * hm_ffn_workspace_bytes(f, M): decode rows (M <= 16) of the Llama-3-8B and Qwen2.5-14B layers need about
+ * 3.3 MB; prefill rows (M > 16) need more than the scratch and return HM_WORKSPACE_TOO_SMALL, as does any
+ * request above HM_STATIC_SCRATCH_BYTES. Calls on one GPU share its scratch: calls that overlap in time on one
+ * GPU (different streams or threads) race; calls on one stream are ordered and safe. */
+#define HM_STATIC_SCRATCH_BYTES (8u << 20)
+hm_status hm_ffn_forward_static(const hm_ffn *f, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t ch_begin,
+                                int64_t ch_end, void *stream);
+
 /* The first half alone: act [M, ch_end - ch_begin] (ld_act) = SiLU(x Wg) * (x Wu). */
 hm_status hm_ffn_gate_up(const hm_ffn *f, void *act, int64_t ld_act, const void *x, int64_t ldx, int64_t M,
                          int64_t ch_begin, int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream);
