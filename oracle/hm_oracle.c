@@ -16,10 +16,15 @@
  *     (:255-281) when the CPU lacks AVX-512. This is the reported CPU baseline.
  *   - the model-path SwiGLU between the CPU GEMVs: torch::silu_ then mul_ on bf16
  *     (src/unified_llm_w4a16_hetero/unified_llm_w4a16.cpp:2881-2883), each rounding to bf16.
- * Float reference math (dequantize, matmul, SwiGLU, RMSNorm) lives in oracle/oracle.py (numpy, float64).
+ *   - a float64 FFN block at one row (RMSNorm, SwiGLU FFN, residual add) with the engine's rounding points,
+ *     for full-size layer stacks without float64 weight matrices in memory.
+ *   - emulations of the rounding points of the reference's GPU kernels (fp16-accumulating decode GEMV,
+ *     bf16-dequantizing prefill GEMM), to attribute disagreements with them.
+ * Float reference math (dequantize, matmul, SwiGLU, RMSNorm) also lives in oracle/oracle.py (numpy, float64).
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <immintrin.h>
@@ -408,4 +413,194 @@ int or_cpu_ffn_decode(const uint16_t *x, const uint8_t *gate, const uint8_t *up,
     or_silu_mul_bf16_model(g, u, inter, threads);
     or_cpu_gemv_packed(g, down, inter, hidden, 0, hidden, y, threads, use_avx);
     return avx;
+}
+
+/* ---- rounding from double ------------------------------------------------------------------------
+ * Direct round to nearest even from a double: rounding to float first and then to 16 bits would round
+ * twice and move values that sit within a float ulp of a 16-bit tie. */
+
+static uint16_t round16_from_f64(double d, int mant_bits, int exp_bias, int max_exp, uint16_t inf_bits, uint16_t nan_bits) {
+    const uint16_t sign = signbit(d) ? 0x8000u : 0u;
+    if (isnan(d)) return (uint16_t)(sign | nan_bits);
+    const double a = fabs(d);
+    if (a == 0.0) return sign;
+    if (isinf(a)) return (uint16_t)(sign | inf_bits);
+    int e;
+    (void)frexp(a, &e);
+    int E = e - 1; /* a = 1.f * 2^E */
+    const int min_exp = 1 - exp_bias;
+    if (E < min_exp) { /* subnormal: quantum 2^(min_exp - mant_bits) */
+        const double r = nearbyint(ldexp(a, mant_bits - min_exp));
+        return (uint16_t)(sign | (uint16_t)r); /* r == 2^mant_bits is the smallest normal's encoding */
+    }
+    double r = nearbyint(ldexp(a, mant_bits - E)); /* in [2^mant_bits, 2^(mant_bits + 1)] */
+    if (r == ldexp(1.0, mant_bits + 1)) {
+        r = ldexp(1.0, mant_bits);
+        ++E;
+    }
+    if (E > max_exp) return (uint16_t)(sign | inf_bits);
+    return (uint16_t)(sign | ((uint32_t)(E + exp_bias) << mant_bits) | ((uint32_t)r - (1u << mant_bits)));
+}
+
+uint16_t or_f16_from_f64(double d) { return round16_from_f64(d, 10, 15, 15, 0x7C00u, 0x7E00u); }
+
+uint16_t or_bf16_from_f64(double d) { return round16_from_f64(d, 7, 127, 127, 0x7F80u, 0x7FC0u); }
+
+static inline double bits_to_f64(uint16_t b, int dtype) { return dtype == 1 ? (double)or_f16_to_f32(b) : (double)or_bf16_to_f32(b); }
+
+static inline uint16_t f64_to_bits(double d, int dtype) { return dtype == 1 ? or_f16_from_f64(d) : or_bf16_from_f64(d); }
+
+static inline double silu_f64(double v) {
+    const double e = exp(-fabs(v));
+    return v >= 0 ? v / (1.0 + e) : v * e / (1.0 + e);
+}
+
+/* out[n] (+)= sum_k x[k] (q[k][n] - z[k / group][n]) s[k / group][n] for n in [n0, n1), in float64, as the
+ * reference's per-tile factorization s (sum q x - z sum x) (kernels/gpu/src/gemv_w4a16.cu:91-98) applied per
+ * group. q [K, N] row-major, s (dtype bits) and z [K / group, N]. */
+static void matvec_f64(const double *x, const uint8_t *q, const uint16_t *s, const uint8_t *z, int64_t K, int64_t N, int64_t group,
+                       int dtype, int64_t n0, int64_t n1, double *out) {
+    const int64_t w = n1 - n0;
+    double p[64];
+    for (int64_t c = 0; c < w; ++c) out[n0 + c] = 0.0;
+    for (int64_t g = 0; g < K / group; ++g) {
+        double xs = 0.0;
+        for (int64_t c = 0; c < w; ++c) p[c] = 0.0;
+        for (int64_t k = g * group; k < (g + 1) * group; ++k) {
+            const uint8_t *row = q + k * N + n0;
+            xs += x[k];
+            for (int64_t c = 0; c < w; ++c) p[c] += x[k] * (double)row[c];
+        }
+        for (int64_t c = 0; c < w; ++c) {
+            const double sc = bits_to_f64(s[g * N + n0 + c], dtype);
+            out[n0 + c] += sc * (p[c] - (double)z[g * N + n0 + c] * xs);
+        }
+    }
+}
+
+/* One pre-norm FFN block at one row in float64 with the engine's rounding points (SwiGLU and RMSNorm numerics of
+ * kernels/gpu/src/silu_mul.cu:10-30 and src/hipkernels/rmsnorm.cu:25-62, layer as unified_llm_w4a16.cpp:2867-2892):
+ *   normed = round(x * rsqrt(mean(x^2) + eps) * w)      (norm_w == NULL: normed = x, no rounding)
+ *   act    = round(SiLU(normed Wg) * (normed Wu))
+ *   y      = round(act Wd),  x_out = round(x + y)
+ * x, norm_w, the scales and every *_bits output are 16-bit `dtype` values (0 bf16, 1 fp16); g_raw, u_raw, y_raw
+ * (may be NULL) receive the unrounded float64 sums. Parallel over 64-column chunks. */
+void or_ffn_block_f64(const uint16_t *x, const uint16_t *norm_w, double eps, const uint8_t *gq, const uint16_t *gs, const uint8_t *gz,
+                      const uint8_t *uq, const uint16_t *us, const uint8_t *uz, const uint8_t *dq, const uint16_t *ds, const uint8_t *dz,
+                      int64_t hidden, int64_t inter, int64_t group, int dtype, int threads, uint16_t *normed_bits, uint16_t *act_bits,
+                      uint16_t *y_bits, uint16_t *x_out_bits, double *g_raw, double *u_raw, double *y_raw) {
+    if (threads < 1) threads = 1;
+    double *xn = (double *)malloc(sizeof(double) * (size_t)hidden);
+    double *g = (double *)malloc(sizeof(double) * (size_t)inter);
+    double *u = (double *)malloc(sizeof(double) * (size_t)inter);
+    double *act = (double *)malloc(sizeof(double) * (size_t)inter);
+    double *y = (double *)malloc(sizeof(double) * (size_t)hidden);
+    double ss = 0.0;
+    for (int64_t k = 0; k < hidden; ++k) {
+        const double v = bits_to_f64(x[k], dtype);
+        ss += v * v;
+    }
+    const double r = 1.0 / sqrt(ss / (double)hidden + eps);
+    for (int64_t k = 0; k < hidden; ++k) {
+        const double v = bits_to_f64(x[k], dtype);
+        if (norm_w != NULL) {
+            const uint16_t b = f64_to_bits(v * r * bits_to_f64(norm_w[k], dtype), dtype);
+            if (normed_bits != NULL) normed_bits[k] = b;
+            xn[k] = bits_to_f64(b, dtype);
+        } else {
+            xn[k] = v;
+        }
+    }
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+    for (int64_t c = 0; c < (inter + 63) / 64; ++c) {
+        const int64_t n0 = c * 64, n1 = n0 + 64 < inter ? n0 + 64 : inter;
+        matvec_f64(xn, gq, gs, gz, hidden, inter, group, dtype, n0, n1, g);
+        matvec_f64(xn, uq, us, uz, hidden, inter, group, dtype, n0, n1, u);
+        for (int64_t n = n0; n < n1; ++n) {
+            const uint16_t b = f64_to_bits(silu_f64(g[n]) * u[n], dtype);
+            act_bits[n] = b;
+            act[n] = bits_to_f64(b, dtype);
+        }
+    }
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+    for (int64_t c = 0; c < (hidden + 63) / 64; ++c) {
+        const int64_t n0 = c * 64, n1 = n0 + 64 < hidden ? n0 + 64 : hidden;
+        matvec_f64(act, dq, ds, dz, inter, hidden, group, dtype, n0, n1, y);
+    }
+    for (int64_t h = 0; h < hidden; ++h) {
+        const uint16_t yb = f64_to_bits(y[h], dtype);
+        y_bits[h] = yb;
+        if (x_out_bits != NULL) x_out_bits[h] = f64_to_bits(bits_to_f64(x[h], dtype) + bits_to_f64(yb, dtype), dtype);
+    }
+    if (g_raw != NULL) memcpy(g_raw, g, sizeof(double) * (size_t)inter);
+    if (u_raw != NULL) memcpy(u_raw, u, sizeof(double) * (size_t)inter);
+    if (y_raw != NULL) memcpy(y_raw, y, sizeof(double) * (size_t)hidden);
+    free(xn);
+    free(g);
+    free(u);
+    free(act);
+    free(y);
+}
+
+/* ---- rounding points of the reference's GPU kernels -----------------------------------------------
+ * These emulate, on the CPU, where the reference's HIP kernels round. They need an RDNA GPU to run, so their
+ * exact output bits cannot be pinned here; the emulations make a disagreement with them attributable. */
+
+/* The reference decode GEMV w4a16_gemv_kernel_packed (src/hipkernels/w4a16_gemv_packed.cu:24-176) on logical
+ * weights: x (bf16) to fp16; scale (bf16) and zero to fp16; w = fp16((q - z) * s); per lane four fp16
+ * accumulators, lane (row b of each 8-row block) taking rows sr * 8 + b of every K tile into accumulator sr % 4
+ * with an fp16 fused multiply-add, K tiles in order; then fp16 (a0 + a1) + (a2 + a3), to fp32, and the shuffle
+ * tree ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)) over the 8 lanes in fp32; bf16 output.
+ * q [K, N], s bf16 bits [K / 128, N], z [K / 128, N]; group 128 (the tile height). */
+void or_hm_gemv_emul(const uint16_t *x_bf16, const uint8_t *q, const uint16_t *s, const uint8_t *z, int64_t K, int64_t N, uint16_t *y_bf16,
+                     int threads) {
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+    for (int64_t n = 0; n < N; ++n) {
+        float v[8];
+        for (int b = 0; b < 8; ++b) {
+            double acc[4] = {0.0, 0.0, 0.0, 0.0}; /* fp16 values */
+            for (int64_t kt = 0; kt < K / 128; ++kt) {
+                const double s16 = (double)or_f16_to_f32(or_f16_from_f32(or_bf16_to_f32(s[kt * N + n])));
+                const double z16 = (double)or_f16_to_f32(or_f16_from_f32((float)(int8_t)z[kt * N + n]));
+                for (int sr = 0; sr < 16; ++sr) {
+                    const int64_t row = kt * 128 + sr * 8 + b;
+                    const double w = (double)or_f16_to_f32(or_f16_from_f64(((double)q[row * N + n] - z16) * s16));
+                    const double xv = (double)or_f16_to_f32(or_f16_from_f32(or_bf16_to_f32(x_bf16[row])));
+                    acc[sr % 4] = (double)or_f16_to_f32(or_f16_from_f64(w * xv + acc[sr % 4]));
+                }
+            }
+            const double a01 = (double)or_f16_to_f32(or_f16_from_f64(acc[0] + acc[1]));
+            const double a23 = (double)or_f16_to_f32(or_f16_from_f64(acc[2] + acc[3]));
+            v[b] = or_f16_to_f32(or_f16_from_f64(a01 + a23));
+        }
+        const float t = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        y_bf16[n] = or_bf16_from_f32(t);
+    }
+}
+
+/* The reference prefill GEMM w4a16_gemm_rocwmma_packed (src/hipkernels/w4a16_gemm_packed.cu:380-613) on logical
+ * weights: each weight rounded once to bf16((q - z) * s) with the product in fp32 (:491-497), bf16 x bf16
+ * products accumulated in fp32 over 16-K steps in K order (one rounding per 16-K step: the sum inside a step
+ * is formed exactly here), fp32 result. q [K, N], s bf16 bits and z [K / group, N], x bf16 [M, K];
+ * out fp32 [M, N]. */
+void or_hm_gemm_emul(const uint16_t *x_bf16, const uint8_t *q, const uint16_t *s, const uint8_t *z, int64_t M, int64_t K, int64_t N,
+                     int64_t group, float *out, int threads) {
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t m = 0; m < M; ++m) {
+            float acc = 0.0f;
+            for (int64_t k0 = 0; k0 < K; k0 += 16) {
+                double step = 0.0;
+                for (int64_t k = k0; k < k0 + 16; ++k) {
+                    const float sc = or_bf16_to_f32(s[(k / group) * N + n]);
+                    const float wv = or_bf16_to_f32(or_bf16_from_f32((float)((int)q[k * N + n] - (int)z[(k / group) * N + n]) * sc));
+                    step += (double)wv * (double)or_bf16_to_f32(x_bf16[m * K + k]);
+                }
+                acc = (float)((double)acc + step);
+            }
+            out[m * N + n] = acc;
+        }
+    }
 }

@@ -47,6 +47,12 @@ def lib():
         L.or_cpu_gemv_packed.argtypes, L.or_cpu_gemv_packed.restype = [P, P, i64, i64, i64, i64, P, ctypes.c_int, ctypes.c_int], ctypes.c_int
         L.or_silu_mul_bf16_model.argtypes = [P, P, i64, ctypes.c_int]
         L.or_cpu_ffn_decode.argtypes, L.or_cpu_ffn_decode.restype = [P, P, P, P, i64, i64, P, P, ctypes.c_int, ctypes.c_int], ctypes.c_int
+        L.or_f16_from_f64.argtypes, L.or_f16_from_f64.restype = [ctypes.c_double], ctypes.c_uint16
+        L.or_bf16_from_f64.argtypes, L.or_bf16_from_f64.restype = [ctypes.c_double], ctypes.c_uint16
+        L.or_ffn_block_f64.argtypes = [P, P, ctypes.c_double, P, P, P, P, P, P, P, P, P, i64, i64, i64, ctypes.c_int, ctypes.c_int,
+                                       P, P, P, P, P, P, P]
+        L.or_hm_gemv_emul.argtypes = [P, P, P, P, i64, i64, P, ctypes.c_int]
+        L.or_hm_gemm_emul.argtypes = [P, P, P, P, i64, i64, i64, i64, P, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -278,6 +284,64 @@ def rmsnorm(x, w, eps):
     """x * rsqrt(mean(x^2) + eps) * w per row (src/hipkernels/rmsnorm.cu:25-62, non-gemma), float64."""
     x = np.asarray(x, np.float64)
     return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+
+
+def _dtype_code(dtype):
+    return 1 if dtype == "fp16" else 0
+
+
+def f64_to_bits(value, dtype):
+    """One float64 value rounded directly (round to nearest even, no intermediate float32) to `dtype` bits."""
+    return int(lib().or_f16_from_f64(float(value)) if dtype == "fp16" else lib().or_bf16_from_f64(float(value)))
+
+
+def ffn_block_f64(x_bits, norm_bits, eps, gate, up, down, group, dtype, threads=8):
+    """One pre-norm FFN block at one row in float64 with the engine's rounding points (C restatement,
+    hm_oracle.c or_ffn_block_f64; rmsnorm.cu:25-62, silu_mul.cu:10-30, unified_llm_w4a16.cpp:2867-2892):
+    normed = round(x rsqrt(mean x^2 + eps) w), act = round(SiLU(normed Wg) (normed Wu)), y = round(act Wd),
+    x_out = round(x + y). norm_bits None: no norm (normed = x). gate/up/down are logical (q, s_bits, z) tuples.
+    Returns a dict of bit arrays (normed, act, y, x_out) and float64 sums (g, u, y_raw)."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint16).ravel()
+    hidden = x_bits.size
+    inter = gate[0].shape[1]
+    keep = [np.ascontiguousarray(t, d) for w in (gate, up, down) for t, d in zip(w, (np.uint8, np.uint16, np.uint8))]
+    args = []
+    for i in range(0, 9, 3):
+        args += [_ptr(keep[i]), _ptr(keep[i + 1]), _ptr(keep[i + 2])]
+    out = {"normed": np.zeros(hidden, np.uint16), "act": np.empty(inter, np.uint16), "y": np.empty(hidden, np.uint16),
+           "x_out": np.empty(hidden, np.uint16), "g": np.empty(inter), "u": np.empty(inter), "y_raw": np.empty(hidden)}
+    nw = None if norm_bits is None else np.ascontiguousarray(norm_bits, np.uint16).ravel()
+    lib().or_ffn_block_f64(_ptr(x_bits), None if nw is None else _ptr(nw), float(eps), *args, hidden, inter, group, _dtype_code(dtype),
+                           threads, _ptr(out["normed"]), _ptr(out["act"]), _ptr(out["y"]), _ptr(out["x_out"]), _ptr(out["g"]), _ptr(out["u"]),
+                           _ptr(out["y_raw"]))
+    return out
+
+
+def hm_gemv_emul(x_bf16_bits, q, s_bf16_bits, z, threads=8):
+    """Emulated rounding points of the reference's decode GEMV (w4a16_gemv_packed.cu:24-176: fp16 weights and fp16
+    accumulation, fp32 lane tree, bf16 output) on logical group-128 weights. x bf16 bits [K] -> bf16 bits [N]."""
+    x = np.ascontiguousarray(x_bf16_bits, np.uint16).ravel()
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(s_bf16_bits, np.uint16)
+    z = np.ascontiguousarray(z, np.uint8)
+    k, n = q.shape
+    y = np.empty(n, np.uint16)
+    lib().or_hm_gemv_emul(_ptr(x), _ptr(q), _ptr(s), _ptr(z), k, n, _ptr(y), threads)
+    return y
+
+
+def hm_gemm_emul(x_bf16_bits, q, s_bf16_bits, z, group=128, threads=8):
+    """Emulated rounding points of the reference's prefill GEMM (w4a16_gemm_packed.cu:380-613: weights rounded once to
+    bf16, fp32 accumulation per 16-K step). x bf16 bits [M, K] -> fp32 [M, N] (before the output rounding)."""
+    x = np.ascontiguousarray(x_bf16_bits, np.uint16)
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(s_bf16_bits, np.uint16)
+    z = np.ascontiguousarray(z, np.uint8)
+    m, k = x.shape
+    n = q.shape[1]
+    out = np.empty((m, n), np.float32)
+    lib().or_hm_gemm_emul(_ptr(x), _ptr(q), _ptr(s), _ptr(z), m, k, n, group, _ptr(out), threads)
+    return out
 
 
 def partition_from_ratio(intermediate, ratio, alignment=128):

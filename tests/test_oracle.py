@@ -311,3 +311,195 @@ def test_rmsnorm_closed_form(oracle):
     w = np.array([1.0, 2.0, 1.0, 1.0])
     got = oracle.rmsnorm(x, w, 0.0)
     np.testing.assert_allclose(got, [[3 / 2.5, 8 / 2.5, 0, 0]], rtol=1e-15)
+
+
+def test_rmsnorm_eps_inside_the_root(oracle):
+    # A row of equal values a: mean(x^2) = a^2, so normed = a / sqrt(a^2 + eps) * w exactly (rmsnorm.cu:48 adds eps
+    # under the square root). At |a| = 1e-3 with eps = 1e-5 that is 0.30151..., far from a / (|a| + eps) = 0.990...
+    # (eps outside the root) and from 1 (eps dropped).
+    a, eps = 1e-3, 1e-5
+    x = np.full((2, 64), a)
+    x[1] *= -1
+    w = np.linspace(0.5, 1.5, 64)
+    got = oracle.rmsnorm(x, w, eps)
+    exp = a / math.sqrt(a * a + eps)
+    np.testing.assert_allclose(got[0], exp * w, rtol=1e-14)
+    np.testing.assert_allclose(got[1], -exp * w, rtol=1e-14)
+    assert abs(exp - 0.30151134457776363) < 1e-15
+
+
+# ---- direct rounding from float64 ---------------------------------------------------------------------
+
+def test_f16_from_f64_matches_numpy_direct_cast(oracle):
+    # numpy converts float64 -> float16 directly from the double's bits (round to nearest even); values within a
+    # float32 ulp of a float16 tie separate a direct rounding from one through float32.
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal(20000) * np.exp(rng.uniform(-25, 12, 20000))
+    ties = np.float16(rng.standard_normal(3000)).astype(np.float64)
+    ulp = np.spacing(np.abs(ties.astype(np.float16))).astype(np.float64)
+    near = np.concatenate([ties + ulp / 2, ties - ulp / 2, ties + ulp / 2 * (1 + 2.0 ** -40), ties + ulp / 2 * (1 - 2.0 ** -40)])
+    vals = np.concatenate([x, near, [0.0, -0.0, 65519.99, 65520.0, 1e-8, -6e-8, 2.0 ** -25, 3 * 2.0 ** -26]])
+    got = np.array([oracle.f64_to_bits(v, "fp16") for v in vals], np.uint16)
+    with np.errstate(over="ignore"):  # 65520 rounds to infinity, as intended
+        np.testing.assert_array_equal(got, vals.astype(np.float16).view(np.uint16))
+
+
+def test_bf16_from_f64_ties(oracle):
+    # 1 + 2^-8 is a bf16 tie (rounds to even: 1.0); 2^-40 above it must round up, which a detour through float32
+    # (where 1 + 2^-8 + 2^-40 becomes the tie itself) would not do.
+    assert oracle.f64_to_bits(1 + 2.0 ** -8, "bf16") == 0x3F80
+    assert oracle.f64_to_bits(1 + 2.0 ** -8 + 2.0 ** -40, "bf16") == 0x3F81
+    assert oracle.f64_to_bits(1 + 3 * 2.0 ** -8, "bf16") == 0x3F82  # tie between 0x3F81 and 0x3F82: even
+    assert oracle.f64_to_bits(-3.0234375, "bf16") == 0xC042  # -(3 + 3/128): tie, even mantissa 3.03125
+    rng = np.random.default_rng(22)
+    v = (rng.standard_normal(5000) * np.exp(rng.uniform(-20, 20, 5000))).astype(np.float32)
+    got = np.array([oracle.f64_to_bits(float(t), "bf16") for t in v], np.uint16)
+    np.testing.assert_array_equal(got, oracle.bf16_bits(v))  # float32-exact inputs: one rounding either way
+
+
+# ---- float64 FFN block (C) -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,group", [("fp16", 128), ("bf16", 64), ("fp16", 32)])
+def test_ffn_block_f64_matches_numpy(oracle, dtype, group):
+    # The C block against the numpy formulation (dense dequantized matrices, matrix products): the float64 sums
+    # agree to rounding, the rounded activations and outputs bit for bit.
+    rng = np.random.default_rng(31)
+    h, inter = 256, 384
+    gate = oracle.random_weights(rng, h, inter, group, dtype)
+    up = oracle.random_weights(rng, h, inter, group, dtype)
+    down = oracle.random_weights(rng, inter, h, group, dtype)
+    x_bits = oracle.to_bits((rng.standard_normal(h) * 3).astype(np.float32), dtype)
+    w_bits = oracle.to_bits(rng.uniform(0.5, 1.5, h).astype(np.float32), dtype)
+    eps = 1e-5
+    out = oracle.ffn_block_f64(x_bits, w_bits, eps, gate, up, down, group, dtype, threads=2)
+    x = oracle.from_bits(x_bits, dtype).astype(np.float64)
+    normed = oracle.rmsnorm(x[None], oracle.from_bits(w_bits, dtype), eps)[0]
+    normed_bits = np.array([oracle.f64_to_bits(v, dtype) for v in normed], np.uint16)
+    np.testing.assert_array_equal(out["normed"], normed_bits)
+    xn = oracle.from_bits(normed_bits, dtype).astype(np.float64)
+    g = xn @ oracle.weights_f64(*gate, group, dtype)
+    u = xn @ oracle.weights_f64(*up, group, dtype)
+    np.testing.assert_allclose(out["g"], g, rtol=1e-11, atol=1e-11)
+    np.testing.assert_allclose(out["u"], u, rtol=1e-11, atol=1e-11)
+    act_bits = np.array([oracle.f64_to_bits(v, dtype) for v in oracle.silu(out["g"]) * out["u"]], np.uint16)
+    np.testing.assert_array_equal(out["act"], act_bits)
+    y = oracle.from_bits(act_bits, dtype).astype(np.float64) @ oracle.weights_f64(*down, group, dtype)
+    np.testing.assert_allclose(out["y_raw"], y, rtol=1e-11, atol=1e-9)
+    y_bits = np.array([oracle.f64_to_bits(v, dtype) for v in out["y_raw"]], np.uint16)
+    np.testing.assert_array_equal(out["y"], y_bits)
+    x_out = np.array([oracle.f64_to_bits(a + b, dtype) for a, b in zip(x, oracle.from_bits(y_bits, dtype))], np.uint16)
+    np.testing.assert_array_equal(out["x_out"], x_out)
+    # no norm: the block is the plain FFN of x plus the residual
+    plain = oracle.ffn_block_f64(x_bits, None, eps, gate, up, down, group, dtype, threads=2)
+    ref, _ = oracle.ffn(x[None], gate, up, down, group, dtype)
+    np.testing.assert_allclose(plain["y_raw"], ref[0], rtol=1e-9, atol=1e-9)
+
+
+def test_planted_ffn_block_gate_up_swap(oracle):
+    # SiLU(g) u is not symmetric: a block with gate and up exchanged must differ.
+    rng = np.random.default_rng(32)
+    h, inter = 128, 256
+    gate, up, down = (oracle.random_weights(rng, *s, 128, "fp16") for s in ((h, inter), (h, inter), (inter, h)))
+    x_bits = oracle.to_bits(rng.standard_normal(h).astype(np.float32), "fp16")
+    a = oracle.ffn_block_f64(x_bits, None, 0.0, gate, up, down, 128, "fp16", threads=1)
+    b = oracle.ffn_block_f64(x_bits, None, 0.0, up, gate, down, 128, "fp16", threads=1)
+    assert not np.array_equal(a["y"], b["y"])
+
+
+# ---- rounding points of the reference's GPU kernels -------------------------------------------------------
+
+def _bf16(v):
+    return int(np.asarray([v], np.float32).view(np.uint32)[0] >> 16)
+
+
+def test_hm_gemv_emul_constant_case(oracle):
+    # docs/progress.md:457-460: x = 1/16, q = 9, z = 8, s = 1/16, K = 2048 gives exactly 8 (every partial sum is exact).
+    k, n = 2048, 64
+    x = np.full(k, _bf16(1 / 16), np.uint16)
+    q = np.full((k, n), 9, np.uint8)
+    s = np.full((k // 128, n), _bf16(1 / 16), np.uint16)
+    z = np.full((k // 128, n), 8, np.uint8)
+    y = oracle.hm_gemv_emul(x, q, s, z, threads=2)
+    assert np.all(oracle.bf16_bits_to_f32(y) == 8.0)
+
+
+def test_hm_gemv_emul_fp16_accumulation_known_answer(oracle):
+    # Lane b = 0 of the reference GEMV takes rows sr * 8 (sr = 0..15) of each K tile into accumulator sr % 4. With
+    # weights 1 (q = 9, z = 8, s = 1), x[0] = 1 and x = 2^-12 on the other rows 8 j, accumulator 0 holds 1 and each
+    # further 2^-12 is below half an fp16 ulp of 1, so it stays 1; accumulators 1..3 each sum 32 x 2^-12 = 2^-7.
+    # (a0 + a1) + (a2 + a3) = 1 + 2^-7 + 2^-6 = 1.0234375 (bf16-exact), where the exact sum 1 + 127 * 2^-12 rounds
+    # to bf16 1.03125. A GEMV accumulating in fp32 gives 1.03125, one without per-lane accumulators another value.
+    k, n = 1024, 64
+    x = np.zeros(k, np.uint16)
+    x[0::8] = _bf16(2.0 ** -12)
+    x[0] = _bf16(1.0)
+    q = np.full((k, n), 9, np.uint8)
+    s = np.full((k // 128, n), _bf16(1.0), np.uint16)
+    z = np.full((k // 128, n), 8, np.uint8)
+    y = oracle.bf16_bits_to_f32(oracle.hm_gemv_emul(x, q, s, z, threads=2))
+    assert np.all(y == np.float32(1.0234375)), y[:4]
+    exact = 1 + 127 * 2.0 ** -12
+    assert oracle.bf16_round(np.float32(exact)) == np.float32(1.03125)
+
+
+def test_hm_gemv_emul_exact_regime_matches_float64(oracle):
+    # Small integers keep every fp16 partial sum exact, so the emulation equals float64 rounded to bf16: this pins
+    # the row, column and group indexing of the emulation.
+    rng = np.random.default_rng(33)
+    k, n = 512, 192
+    xv = rng.integers(-1, 2, k).astype(np.float32)
+    q = rng.integers(0, 16, (k, n), dtype=np.uint8)
+    z = rng.integers(4, 12, (k // 128, n), dtype=np.uint8)
+    s = np.full((k // 128, n), _bf16(1.0), np.uint16)
+    y = oracle.hm_gemv_emul(oracle.bf16_bits(xv), q, s, z, threads=2)
+    ref = xv.astype(np.float64) @ oracle.dequantize(q, np.ones((k // 128, n)), z, 128)
+    np.testing.assert_array_equal(y, oracle.bf16_bits(ref.astype(np.float32)))
+
+
+def test_hm_gemm_emul_rounds_each_weight_once_to_bf16(oracle):
+    # (q - z) s = 3 * (1 + 2^-7) = 3.0234375 needs 9 significant bits: the reference GEMM stores it as bf16, a tie
+    # that rounds to even (3.03125). With x = 1 on one row the output is that weight; the exact product is not.
+    k, n = 128, 64
+    x = np.zeros((2, k), np.uint16)
+    x[0, 5] = _bf16(1.0)
+    x[1] = _bf16(1 / 16)
+    q = np.full((k, n), 11, np.uint8)
+    z = np.full((1, n), 8, np.uint8)
+    s = np.full((1, n), _bf16(1 + 2.0 ** -7), np.uint16)
+    out = oracle.hm_gemm_emul(x, q, s, z, 128, threads=2)
+    assert np.all(out[0] == np.float32(3.03125))
+    assert np.all(out[1] == np.float32(3.03125 * 128 / 16))
+
+
+def test_hm_gemm_emul_exact_regime_matches_float64(oracle):
+    rng = np.random.default_rng(34)
+    m, k, n, g = 3, 256, 128, 64
+    xv = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    q = rng.integers(0, 16, (k, n), dtype=np.uint8)
+    z = rng.integers(0, 16, (k // g, n), dtype=np.uint8)
+    s = np.full((k // g, n), _bf16(0.5), np.uint16)
+    out = oracle.hm_gemm_emul(oracle.bf16_bits(xv), q, s, z, g, threads=2)
+    ref = xv.astype(np.float64) @ oracle.dequantize(q, np.full((k // g, n), 0.5), z, g)
+    np.testing.assert_array_equal(out, ref.astype(np.float32))
+
+
+def test_cpu_baseline_llama32_1b_shape(oracle):
+    # the restated reference AVX CPU path at the Llama-3.2-1B shape (H = 2048, I = 8192, g = 128,
+    # bf16). Each GEMV as the reference checks it (test_layout_cpu.cpp:128-139: x = rand * 0.1, torch.allclose with
+    # rtol 0.01, atol 0.1 against a dense matmul), then the whole decode FFN (gate, up, silu_ and mul_ in bf16,
+    # down) against the float64 oracle by relative error.
+    rng = np.random.default_rng(35)
+    h, inter = 2048, 8192
+    gate, up, down = (oracle.random_weights(rng, *s, 128, "bf16") for s in ((h, inter), (h, inter), (inter, h)))
+    tiles = [oracle.pack_tiles(*w) for w in (gate, up, down)]
+    for w, t, (k, n) in ((gate, tiles[0], (h, inter)), (down, tiles[2], (inter, h))):
+        xb = oracle.to_bits((rng.uniform(0, 1, k) * 0.1).astype(np.float32), "bf16")
+        y, _ = oracle.cpu_gemv_packed(xb, t, k, n, threads=4)
+        ref = oracle.bf16_bits_to_f32(xb).astype(np.float64) @ oracle.weights_f64(*w, 128, "bf16")
+        np.testing.assert_allclose(oracle.bf16_bits_to_f32(y), ref, rtol=0.01, atol=0.1)
+    x_bits = oracle.to_bits(rng.standard_normal(h).astype(np.float32), "bf16")
+    y, branch = oracle.cpu_ffn_decode(x_bits, *tiles, h, inter, threads=4)
+    ref, _ = oracle.ffn(oracle.bf16_bits_to_f32(x_bits)[None, :].astype(np.float64), gate, up, down, 128, "bf16")
+    e = oracle.errors(oracle.bf16_bits_to_f32(y), ref[0])
+    print(f"config 1 CPU FFN decode ({'AVX-512' if branch else 'scalar'}): {e}")
+    assert e["max_rel"] < 2e-2 and e["rel_l2"] < 1e-2, e
