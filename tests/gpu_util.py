@@ -18,11 +18,12 @@ TORCH = {"fp16": torch.float16, "bf16": torch.bfloat16}
 
 
 def dev(a, device):
-    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    # a fresh copy: a view such as a[None, :] has a zero stride that from_numpy would keep
+    return torch.from_numpy(np.array(a, order="C", copy=True)).to(device)
 
 
 def dev_bits(bits, dtype, device):
-    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(TORCH[dtype]).to(device)
+    return torch.from_numpy(np.array(bits, np.uint16, order="C", copy=True).view(np.int16)).view(TORCH[dtype]).to(device)
 
 
 def host_f64(t):
