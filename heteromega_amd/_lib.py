@@ -57,6 +57,8 @@ _SIGNATURES = {
     "hm_gptq_unpack_zeros": (ctypes.c_int, [P, I64, I64, I32, P]),
     "hm_weights_from_tiles": (ctypes.c_int, [P, I64, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_weights_from_logical": (ctypes.c_int, [P, P, P, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
+    "hm_weights_from_gate_up_tiles": (ctypes.c_int, [P, I64, I64, I64, I64, I32, ctypes.c_int, P, ctypes.POINTER(P)]),
+    "hm_weights_dequantize": (ctypes.c_int, [P, P, I64, I32, P]),
     "hm_weights_to_logical": (ctypes.c_int, [P, P, P, P, P]),
     "hm_weights_info": (ctypes.c_int, [P, ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(I32),
                                        ctypes.POINTER(I64)]),
@@ -65,10 +67,13 @@ _SIGNATURES = {
     "hm_weights_concat": (ctypes.c_int, [ctypes.POINTER(P), ctypes.c_int32, P, ctypes.POINTER(P)]),
     "hm_linear_workspace_bytes": (SZ, [P, I64, I64, I64]),
     "hm_linear": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I64, I64, P, SZ, P]),
+    "hm_linear_swiglu_workspace_bytes": (SZ, [P, I64, I64, I64]),
+    "hm_linear_swiglu": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I64, I64, P, SZ, P]),
     "hm_linear_k_split_workspace_bytes": (SZ, [P, P, I64, I64, I64, I64]),
     "hm_linear_k_split": (ctypes.c_int, [P, P, P, I64, P, I64, I64, I64, I64, I64, P, SZ, P]),
     "hm_ffn_from_tiles": (ctypes.c_int, [P, P, P, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_ffn_from_tiles_padded": (ctypes.c_int, [P, P, P, I64, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
+    "hm_ffn_from_gate_up_tiles": (ctypes.c_int, [P, P, I64, I64, I64, I32, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_ffn_from_logical": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, ctypes.c_int, P, ctypes.POINTER(P)]),
     "hm_ffn_info": (ctypes.c_int, [P, ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(I32)]),
     "hm_ffn_destroy": (ctypes.c_int, [P]),

@@ -55,6 +55,48 @@ def _compile(src, verbose):
     return obj
 
 
+SHIM_DIR = os.path.join(HERE, "shim")
+SHIM_SOURCES = ["hm_reference_api.cpp", "py_module.cpp"]
+SHIM_NAME = "_reference_shim"
+
+
+def build_shim(verbose=False):
+    """The reference-signature C++ operators (shim/hm_reference_api.cpp) against torch's C++ headers, as a Python
+    module over libhmw4a16.so. Host code only (g++): it calls the C ABI and launches nothing itself."""
+    import sysconfig
+
+    import torch.utils.cpp_extension as ext
+
+    torch_lib = ext.library_paths()[0]
+    out = os.path.join(HERE, SHIM_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+    import torch
+
+    flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+             f"-DTORCH_EXTENSION_NAME={SHIM_NAME}", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", f"-I{sysconfig.get_paths()['include']}",
+             *[f"-I{p}" for p in ext.include_paths()], f"-I{os.path.join(ROOT, 'include')}"]
+    os.makedirs(BUILD_DIR, exist_ok=True)
+
+    def compile_one(src):
+        obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+        cmd = ["g++", *flags, "-c", os.path.join(SHIM_DIR, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"shim build failed on {src}:\n{res.stdout}\n{res.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=len(SHIM_SOURCES)) as pool:
+        objs = list(pool.map(compile_one, SHIM_SOURCES))
+    cmd = ["g++", "-shared", *objs, f"-L{torch_lib}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", f"-L{HERE}", "-lhmw4a16",
+           "-L/opt/rocm/lib", "-lamdhip64", f"-Wl,-rpath,{torch_lib}", "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"shim link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(verbose=False):
     os.makedirs(BUILD_DIR, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as pool:
@@ -72,3 +114,5 @@ def build(verbose=False):
 
 if __name__ == "__main__":
     print(build(verbose="--verbose" in sys.argv))
+    if "--no-shim" not in sys.argv:
+        print(build_shim(verbose="--verbose" in sys.argv))

@@ -17,6 +17,8 @@ struct hm_weights {
     void *buffer = nullptr;
     int64_t bytes = 0;
     int64_t quant_bytes = 0, meta_bytes = 0;
+    uint32_t *status = nullptr; // device word after the planes: the repack's out-of-range zero flag
+    bool fused = false;         // gate_up: strips alternate gate / up per 16 channels (N = 2 x channels)
 };
 
 struct hm_ffn {
@@ -65,7 +67,8 @@ hm_status alloc_planes(hm_weights *w, int64_t K, int64_t N, int64_t group, int d
     w->quant_bytes = K * N / 2;
     w->meta_bytes = (N / 16) * (K / group) * 16 * 4;
     const int64_t meta_off = round_up(w->quant_bytes, 256);
-    w->bytes = meta_off + w->meta_bytes;
+    const int64_t status_off = round_up(meta_off + w->meta_bytes, 256);
+    w->bytes = status_off + 256;
     const hipError_t e = hipMalloc(&w->buffer, static_cast<size_t>(w->bytes));
     if (e != hipSuccess) {
         w->buffer = nullptr;
@@ -73,6 +76,31 @@ hm_status alloc_planes(hm_weights *w, int64_t K, int64_t N, int64_t group, int d
     }
     w->p.quant = static_cast<const uint8_t *>(w->buffer);
     w->p.meta = reinterpret_cast<const uint32_t *>(static_cast<uint8_t *>(w->buffer) + meta_off);
+    w->status = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(w->buffer) + status_off);
+    return HM_OK;
+}
+
+// Clears the zero-point flag before a repack (load time only, never inside a captured graph).
+hm_status begin_repack(hm_weights *w, hipStream_t s) {
+    const hipError_t e = hipMemsetAsync(w->status, 0, sizeof(uint32_t), s);
+    return e == hipSuccess ? HM_OK : hip_fail(e, "clearing the repack status");
+}
+
+// Waits for the repack and reports zero points outside 0..16: the kernels read zeros as unsigned bytes and build
+// 1024 + z and 1024 + 16 z in fp16, exact only for small z; the reference's GPU reads tile zeros as int8
+// (w4a16_gemv_packed.cu:86-87) and its CPU as uint8 (w4a16_gemv_avx_packed.cpp:122-124), which agree on 0..127.
+hm_status end_repack(const hm_weights *w, hipStream_t s, const char *what) {
+    uint32_t flag = 0;
+    hipError_t e = hipMemcpyAsync(&flag, w->status, sizeof(flag), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) {
+        e = hipStreamSynchronize(s);
+    }
+    if (e != hipSuccess) {
+        return hip_fail(e, "repack");
+    }
+    if (flag != 0) {
+        return fail(HM_INVALID_ARGUMENT, "%s: zero points must lie in 0..%u", what, hm::kMaxZero);
+    }
     return HM_OK;
 }
 
@@ -104,6 +132,37 @@ hm_status check_tile_source(const uint8_t *tiles, int64_t packed_k, int64_t pack
                     static_cast<long long>(packed_n));
     }
     return HM_OK;
+}
+
+// A reference gate_up matrix packed [packed_k, 2 stored] in `layout` order (kernels/gpu/include/heteromega/gpu_ffn.hpp:
+// 43-71: FfnSliceWeights.gate_up); the engine takes channels [0, channels) over K rows.
+hm_status check_gate_up_source(const uint8_t *gate_up, int64_t packed_k, int64_t stored, int64_t K, int64_t channels, int32_t layout,
+                               const char *what) {
+    if (layout != HM_GATE_UP_BLOCKED && layout != HM_GATE_UP_INTERLEAVED) {
+        return fail(HM_INVALID_ARGUMENT, "%s: layout must be HM_GATE_UP_BLOCKED or HM_GATE_UP_INTERLEAVED, got %d", what, static_cast<int>(layout));
+    }
+    if (stored <= 0 || stored % 64) {
+        return fail(HM_INVALID_ARGUMENT, "%s: stored channels %lld must be a positive multiple of 64", what, static_cast<long long>(stored));
+    }
+    if (channels <= 0 || channels % 16 || channels > stored) {
+        return fail(HM_INVALID_ARGUMENT, "%s: channels %lld must be a positive multiple of 16 within the %lld stored", what,
+                    static_cast<long long>(channels), static_cast<long long>(stored));
+    }
+    return check_tile_source(gate_up, packed_k, 2 * stored, K, 2 * channels, what);
+}
+
+// The gate and up halves of a reference gate_up matrix as the two sources of a fused repack.
+void gate_up_sources(const uint8_t *gate_up, int64_t packed_k, int64_t stored, int32_t layout, hm::TileSource gu[2]) {
+    for (int i = 0; i < 2; ++i) {
+        gu[i].tiles = gate_up;
+        gu[i].tiles_k = packed_k / 128;
+        gu[i].tiles_n = 2 * stored / 64;
+        if (layout == HM_GATE_UP_INTERLEAVED) {
+            gu[i].col_mode = 1 + i; // per 64 channels: 64 gate columns, then 64 up columns
+        } else {
+            gu[i].col_offset = i * stored; // [gate 0..stored) | up 0..stored)]
+        }
+    }
 }
 
 hm_status check_logical(const uint8_t *q, const uint16_t *s, const uint8_t *z, int64_t K, int64_t N, int64_t group,
@@ -233,6 +292,82 @@ hm_status check_channels(const hm_ffn *f, int64_t b, int64_t e) {
 
 } // namespace
 
+namespace {
+
+hm_status check_ffn_shape(int64_t hidden, int64_t inter, const char *what) {
+    if (hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128) {
+        return fail(HM_INVALID_ARGUMENT, "%s: hidden and inter must be positive multiples of 128, got %lld, %lld", what,
+                    static_cast<long long>(hidden), static_cast<long long>(inter));
+    }
+    return HM_OK;
+}
+
+void destroy_ffn(hm_ffn *f) {
+    free_planes(&f->gate_up);
+    free_planes(&f->down);
+    delete f;
+}
+
+// An FFN layer with both planes allocated (gate_up [H, 2 I] fused, down [I, H]).
+hm_status new_ffn(int64_t hidden, int64_t inter, int64_t group, hm_dtype dtype, hm_ffn **out) {
+    auto *f = new hm_ffn;
+    f->hidden = hidden;
+    f->inter = inter;
+    hm_status st = alloc_planes(&f->gate_up, hidden, 2 * inter, group, dtype);
+    if (st == HM_OK && (st = alloc_planes(&f->down, inter, hidden, group, dtype)) != HM_OK) {
+        free_planes(&f->gate_up);
+    }
+    if (st != HM_OK) {
+        delete f;
+        return st;
+    }
+    f->gate_up.fused = true;
+    *out = f;
+    return HM_OK;
+}
+
+// Runs the repack launches of a new layer (launches(flag) enqueues them with the zero-point flag), waits for them
+// and publishes the layer, or frees it on any failure.
+template <class Launches> hm_status fill_ffn(hm_ffn *f, hipStream_t s, const char *what, hm_ffn **out, Launches launches) {
+    hm_status st = begin_repack(&f->gate_up, s);
+    if (st == HM_OK) {
+        const hipError_t e = launches(f->gate_up.status);
+        st = e != hipSuccess ? hip_fail(e, "repack launch") : end_repack(&f->gate_up, s, what);
+    }
+    if (st != HM_OK) {
+        destroy_ffn(f);
+        return st;
+    }
+    *out = f;
+    return HM_OK;
+}
+
+// gate_up from two tile sources (separate gate and up matrices, or the halves of one gate_up matrix), down from a
+// packed [down_k, down_n] matrix whose leading [inter, hidden] block is the layer's.
+hm_status build_ffn_from_tiles(const hm::TileSource gu[2], const uint8_t *down, int64_t down_k, int64_t down_n, int64_t hidden, int64_t inter,
+                               hm_dtype dtype, hipStream_t s, const char *what, hm_ffn **out) {
+    hm_ffn *f = nullptr;
+    hm_status st = new_ffn(hidden, inter, 128, dtype, &f);
+    if (st != HM_OK) {
+        return st;
+    }
+    hm::TileSource d;
+    d.tiles = down;
+    d.tiles_k = down_k / 128;
+    d.tiles_n = down_n / 64;
+    return fill_ffn(f, s, what, out, [&](uint32_t *flag) {
+        hipError_t e = hm::launch_repack_tiles(gu, 2, true, const_cast<uint8_t *>(f->gate_up.p.quant), const_cast<uint32_t *>(f->gate_up.p.meta),
+                                               hidden, 2 * inter, dtype, flag, s);
+        if (e == hipSuccess) {
+            e = hm::launch_repack_tiles(&d, 1, false, const_cast<uint8_t *>(f->down.p.quant), const_cast<uint32_t *>(f->down.p.meta), inter,
+                                        hidden, dtype, flag, s);
+        }
+        return e;
+    });
+}
+
+} // namespace
+
 hm_status hm::set_error(hm_status s, const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -272,6 +407,12 @@ hm_status hm_pack_w4a16(const uint8_t *q, const uint16_t *scales, const int8_t *
     if (K <= 0 || N <= 0 || K % 128 || N % 64) {
         return fail(HM_INVALID_ARGUMENT, "hm_pack_w4a16: K must be a multiple of 128 and N of 64, got %lldx%lld",
                     static_cast<long long>(K), static_cast<long long>(N));
+    }
+    for (int64_t i = 0; i < (K / 128) * N; ++i) {
+        if (zeros[i] < 0 || zeros[i] > static_cast<int>(hm::kMaxZero)) {
+            return fail(HM_INVALID_ARGUMENT, "hm_pack_w4a16: zero point %d at [%lld, %lld] is outside 0..%u", static_cast<int>(zeros[i]),
+                        static_cast<long long>(i / N), static_cast<long long>(i % N), hm::kMaxZero);
+        }
     }
     const int64_t tiles_k = K / 128, tiles_n = N / 64;
     for (int64_t c = 0; c < tiles_n; ++c) {
@@ -359,12 +500,16 @@ hm_status hm_weights_from_tiles(const uint8_t *tiles, int64_t packed_k, int64_t 
     src.tiles = tiles;
     src.tiles_k = packed_k / 128;
     src.tiles_n = packed_n / 64;
-    const hipError_t e = hm::launch_repack_tiles(&src, 1, false, const_cast<uint8_t *>(w->p.quant), const_cast<uint32_t *>(w->p.meta), K,
-                                                 N, dtype, as_stream(stream));
-    if (e != hipSuccess) {
+    const hipStream_t s = as_stream(stream);
+    if ((st = begin_repack(w, s)) == HM_OK) {
+        const hipError_t e = hm::launch_repack_tiles(&src, 1, false, const_cast<uint8_t *>(w->p.quant), const_cast<uint32_t *>(w->p.meta), K,
+                                                     N, dtype, w->status, s);
+        st = e != hipSuccess ? hip_fail(e, "repack launch") : end_repack(w, s, "hm_weights_from_tiles");
+    }
+    if (st != HM_OK) {
         free_planes(w);
         delete w;
-        return hip_fail(e, "repack launch");
+        return st;
     }
     *out = w;
     return HM_OK;
@@ -390,15 +535,66 @@ hm_status hm_weights_from_logical(const uint8_t *q, const uint16_t *scales, cons
     src.scales = scales;
     src.zeros = zeros;
     src.ld = N;
-    const hipError_t e = hm::launch_repack_logical(&src, 1, false, const_cast<uint8_t *>(w->p.quant), const_cast<uint32_t *>(w->p.meta), K,
-                                                   N, group, as_stream(stream));
-    if (e != hipSuccess) {
+    const hipStream_t s = as_stream(stream);
+    if ((st = begin_repack(w, s)) == HM_OK) {
+        const hipError_t e = hm::launch_repack_logical(&src, 1, false, const_cast<uint8_t *>(w->p.quant), const_cast<uint32_t *>(w->p.meta),
+                                                       K, N, group, w->status, s);
+        st = e != hipSuccess ? hip_fail(e, "repack launch") : end_repack(w, s, "hm_weights_from_logical");
+    }
+    if (st != HM_OK) {
         free_planes(w);
         delete w;
-        return hip_fail(e, "repack launch");
+        return st;
     }
     *out = w;
     return HM_OK;
+}
+
+hm_status hm_weights_from_gate_up_tiles(const uint8_t *gate_up, int64_t packed_k, int64_t stored, int64_t K, int64_t channels,
+                                        int32_t layout, hm_dtype dtype, void *stream, hm_weights **out) {
+    if (out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_from_gate_up_tiles: null output handle");
+    }
+    *out = nullptr;
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK || (st = check_gate_up_source(gate_up, packed_k, stored, K, channels, layout, "hm_weights_from_gate_up_tiles")) != HM_OK) {
+        return st;
+    }
+    auto *w = new hm_weights;
+    if ((st = alloc_planes(w, K, 2 * channels, 128, dtype)) != HM_OK) {
+        delete w;
+        return st;
+    }
+    w->fused = true;
+    hm::TileSource gu[2];
+    gate_up_sources(gate_up, packed_k, stored, layout, gu);
+    const hipStream_t s = as_stream(stream);
+    if ((st = begin_repack(w, s)) == HM_OK) {
+        const hipError_t e = hm::launch_repack_tiles(gu, 2, true, const_cast<uint8_t *>(w->p.quant), const_cast<uint32_t *>(w->p.meta), K,
+                                                     2 * channels, dtype, w->status, s);
+        st = e != hipSuccess ? hip_fail(e, "repack launch") : end_repack(w, s, "hm_weights_from_gate_up_tiles");
+    }
+    if (st != HM_OK) {
+        free_planes(w);
+        delete w;
+        return st;
+    }
+    *out = w;
+    return HM_OK;
+}
+
+hm_status hm_weights_dequantize(const hm_weights *w, void *out, int64_t ld_out, int32_t transposed, void *stream) {
+    if (w == nullptr || out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_weights_dequantize: null pointer");
+    }
+    const int64_t width = transposed ? w->p.K : w->p.N;
+    if (ld_out < width || (transposed && (ld_out % 8 || !aligned(out, 16))) || !aligned(out, 2)) {
+        return fail(HM_INVALID_ARGUMENT,
+                    "hm_weights_dequantize: leading dimension %lld must be >= %lld (and, transposed, a multiple of 8 with 16-byte alignment)",
+                    static_cast<long long>(ld_out), static_cast<long long>(width));
+    }
+    const hipError_t e = hm::launch_dequantize(w->p, static_cast<uint16_t *>(out), ld_out, transposed != 0, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "dequantize launch");
 }
 
 hm_status hm_weights_to_logical(const hm_weights *w, uint8_t *q, uint16_t *scales, uint8_t *zeros, void *stream) {
@@ -454,6 +650,9 @@ hm_status hm_weights_concat(const hm_weights *const *parts, int32_t count, void 
         if (w == nullptr) {
             return fail(HM_INVALID_ARGUMENT, "hm_weights_concat: part %d is null", static_cast<int>(i));
         }
+        if (w->fused) {
+            return fail(HM_INVALID_ARGUMENT, "hm_weights_concat: part %d is a fused gate_up matrix", static_cast<int>(i));
+        }
         if (w->p.K != parts[0]->p.K || w->p.group != parts[0]->p.group || w->p.dtype != parts[0]->p.dtype) {
             return fail(HM_INVALID_ARGUMENT, "hm_weights_concat: part %d has K %lld, group %lld, dtype %d; part 0 has %lld, %lld, %d",
                         static_cast<int>(i), static_cast<long long>(w->p.K), static_cast<long long>(w->p.group), w->p.dtype,
@@ -501,6 +700,9 @@ hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, in
     if (w == nullptr) {
         return fail(HM_INVALID_ARGUMENT, "hm_linear: null weights");
     }
+    if (w->fused) {
+        return fail(HM_INVALID_ARGUMENT, "hm_linear: a fused gate_up matrix runs through hm_linear_swiglu");
+    }
     if (M <= 0 || k <= 0 || n <= 0 || k % 128 || n % 16 || col_begin < 0 || col_begin % 16 || k > w->p.K || col_begin + n > w->p.N) {
         return fail(HM_INVALID_ARGUMENT, "hm_linear: block k=%lld, columns [%lld, %lld) must be multiples of 128 / 16 inside [%lld, %lld]",
                     static_cast<long long>(k), static_cast<long long>(col_begin), static_cast<long long>(col_begin + n),
@@ -511,6 +713,32 @@ hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, in
         return st;
     }
     return run_linear(w->p, y, ldy, x, ldx, M, col_begin / 16, n, 0, k / 128, false, workspace, workspace_bytes, as_stream(stream));
+}
+
+size_t hm_linear_swiglu_workspace_bytes(const hm_weights *w, int64_t M, int64_t k, int64_t channels) {
+    if (w == nullptr || !w->fused || M <= 0 || k <= 0 || channels <= 0) {
+        return 0;
+    }
+    return linear_workspace(w->p, M, channels, k / 128, true);
+}
+
+hm_status hm_linear_swiglu(const hm_weights *w, void *act, int64_t ld_act, const void *x, int64_t ldx, int64_t M, int64_t k, int64_t ch_begin,
+                           int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream) {
+    if (w == nullptr || !w->fused) {
+        return fail(HM_INVALID_ARGUMENT, "hm_linear_swiglu: needs a fused gate_up matrix (hm_weights_from_gate_up_tiles)");
+    }
+    const int64_t channels = w->p.N / 2;
+    if (M <= 0 || k <= 0 || k % 128 || k > w->p.K || ch_begin < 0 || ch_begin >= ch_end || ch_end > channels || ch_begin % 16 || ch_end % 16) {
+        return fail(HM_INVALID_ARGUMENT, "hm_linear_swiglu: k=%lld (multiple of 128, <= %lld) and channels [%lld, %lld) (multiples of 16 within %lld)",
+                    static_cast<long long>(k), static_cast<long long>(w->p.K), static_cast<long long>(ch_begin), static_cast<long long>(ch_end),
+                    static_cast<long long>(channels));
+    }
+    hm_status st = check_activation(x, ldx, k, "hm_linear_swiglu x");
+    if (st != HM_OK || (st = check_output(act, ld_act, ch_end - ch_begin, "hm_linear_swiglu act")) != HM_OK) {
+        return st;
+    }
+    return run_linear(w->p, act, ld_act, x, ldx, M, 2 * (ch_begin / 16), ch_end - ch_begin, 0, k / 128, true, workspace, workspace_bytes,
+                      as_stream(stream));
 }
 
 size_t hm_linear_k_split_workspace_bytes(const hm_weights *w0, const hm_weights *w1, int64_t M, int64_t k0, int64_t k1, int64_t n) {
@@ -586,28 +814,12 @@ hm_status hm_ffn_from_tiles_padded(const uint8_t *gate, const uint8_t *up, const
     }
     *out = nullptr;
     hm_status st = check_dtype(dtype);
-    if (st != HM_OK) {
+    if (st != HM_OK || (st = check_ffn_shape(hidden, inter, "hm_ffn_from_tiles")) != HM_OK) {
         return st;
-    }
-    if (hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128) {
-        return fail(HM_INVALID_ARGUMENT, "hm_ffn_from_tiles: hidden and inter must be positive multiples of 128, got %lld, %lld",
-                    static_cast<long long>(hidden), static_cast<long long>(inter));
     }
     if ((st = check_tile_source(gate, packed_hidden, packed_inter, hidden, inter, "gate")) != HM_OK ||
         (st = check_tile_source(up, packed_hidden, packed_inter, hidden, inter, "up")) != HM_OK ||
         (st = check_tile_source(down, packed_inter, packed_hidden, inter, hidden, "down")) != HM_OK) {
-        return st;
-    }
-    auto *f = new hm_ffn;
-    f->hidden = hidden;
-    f->inter = inter;
-    if ((st = alloc_planes(&f->gate_up, hidden, 2 * inter, 128, dtype)) != HM_OK) {
-        delete f;
-        return st;
-    }
-    if ((st = alloc_planes(&f->down, inter, hidden, 128, dtype)) != HM_OK) {
-        free_planes(&f->gate_up);
-        delete f;
         return st;
     }
     hm::TileSource gu[2];
@@ -615,24 +827,24 @@ hm_status hm_ffn_from_tiles_padded(const uint8_t *gate, const uint8_t *up, const
     gu[1].tiles = up;
     gu[0].tiles_k = gu[1].tiles_k = packed_hidden / 128;
     gu[0].tiles_n = gu[1].tiles_n = packed_inter / 64;
-    hm::TileSource d;
-    d.tiles = down;
-    d.tiles_k = packed_inter / 128;
-    d.tiles_n = packed_hidden / 64;
-    hipError_t e = hm::launch_repack_tiles(gu, 2, true, const_cast<uint8_t *>(f->gate_up.p.quant), const_cast<uint32_t *>(f->gate_up.p.meta),
-                                           hidden, 2 * inter, dtype, as_stream(stream));
-    if (e == hipSuccess) {
-        e = hm::launch_repack_tiles(&d, 1, false, const_cast<uint8_t *>(f->down.p.quant), const_cast<uint32_t *>(f->down.p.meta), inter,
-                                    hidden, dtype, as_stream(stream));
+    return build_ffn_from_tiles(gu, down, packed_inter, packed_hidden, hidden, inter, dtype, as_stream(stream), "hm_ffn_from_tiles", out);
+}
+
+hm_status hm_ffn_from_gate_up_tiles(const uint8_t *gate_up, const uint8_t *down, int64_t hidden, int64_t inter, int64_t stored, int32_t layout,
+                                    hm_dtype dtype, void *stream, hm_ffn **out) {
+    if (out == nullptr) {
+        return fail(HM_INVALID_ARGUMENT, "hm_ffn_from_gate_up_tiles: null output handle");
     }
-    if (e != hipSuccess) {
-        free_planes(&f->gate_up);
-        free_planes(&f->down);
-        delete f;
-        return hip_fail(e, "repack launch");
+    *out = nullptr;
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK || (st = check_ffn_shape(hidden, inter, "hm_ffn_from_gate_up_tiles")) != HM_OK ||
+        (st = check_gate_up_source(gate_up, hidden, stored, hidden, inter, layout, "gate_up")) != HM_OK ||
+        (st = check_tile_source(down, stored, hidden, inter, hidden, "down")) != HM_OK) {
+        return st;
     }
-    *out = f;
-    return HM_OK;
+    hm::TileSource gu[2];
+    gate_up_sources(gate_up, hidden, stored, layout, gu);
+    return build_ffn_from_tiles(gu, down, stored, hidden, hidden, inter, dtype, as_stream(stream), "hm_ffn_from_gate_up_tiles", out);
 }
 
 hm_status hm_ffn_from_logical(const uint8_t *gate_q, const uint16_t *gate_s, const uint8_t *gate_z, const uint8_t *up_q, const uint16_t *up_s,
@@ -648,16 +860,8 @@ hm_status hm_ffn_from_logical(const uint8_t *gate_q, const uint16_t *gate_s, con
         (st = check_logical(down_q, down_s, down_z, inter, hidden, group, "down")) != HM_OK) {
         return st;
     }
-    auto *f = new hm_ffn;
-    f->hidden = hidden;
-    f->inter = inter;
-    if ((st = alloc_planes(&f->gate_up, hidden, 2 * inter, group, dtype)) != HM_OK) {
-        delete f;
-        return st;
-    }
-    if ((st = alloc_planes(&f->down, inter, hidden, group, dtype)) != HM_OK) {
-        free_planes(&f->gate_up);
-        delete f;
+    hm_ffn *f = nullptr;
+    if ((st = new_ffn(hidden, inter, group, dtype, &f)) != HM_OK) {
         return st;
     }
     hm::LogicalSource gu[2];
@@ -673,20 +877,16 @@ hm_status hm_ffn_from_logical(const uint8_t *gate_q, const uint16_t *gate_s, con
     d.scales = down_s;
     d.zeros = down_z;
     d.ld = hidden;
-    hipError_t e = hm::launch_repack_logical(gu, 2, true, const_cast<uint8_t *>(f->gate_up.p.quant),
-                                             const_cast<uint32_t *>(f->gate_up.p.meta), hidden, 2 * inter, group, as_stream(stream));
-    if (e == hipSuccess) {
-        e = hm::launch_repack_logical(&d, 1, false, const_cast<uint8_t *>(f->down.p.quant), const_cast<uint32_t *>(f->down.p.meta), inter,
-                                      hidden, group, as_stream(stream));
-    }
-    if (e != hipSuccess) {
-        free_planes(&f->gate_up);
-        free_planes(&f->down);
-        delete f;
-        return hip_fail(e, "repack launch");
-    }
-    *out = f;
-    return HM_OK;
+    const hipStream_t s = as_stream(stream);
+    return fill_ffn(f, s, "hm_ffn_from_logical", out, [&](uint32_t *flag) {
+        hipError_t e = hm::launch_repack_logical(gu, 2, true, const_cast<uint8_t *>(f->gate_up.p.quant),
+                                                 const_cast<uint32_t *>(f->gate_up.p.meta), hidden, 2 * inter, group, flag, s);
+        if (e == hipSuccess) {
+            e = hm::launch_repack_logical(&d, 1, false, const_cast<uint8_t *>(f->down.p.quant), const_cast<uint32_t *>(f->down.p.meta), inter,
+                                          hidden, group, flag, s);
+        }
+        return e;
+    });
 }
 
 hm_status hm_ffn_info(const hm_ffn *f, int64_t *hidden, int64_t *inter, int64_t *group, int32_t *dtype) {
@@ -702,9 +902,7 @@ hm_status hm_ffn_info(const hm_ffn *f, int64_t *hidden, int64_t *inter, int64_t 
 
 hm_status hm_ffn_destroy(hm_ffn *f) {
     if (f != nullptr) {
-        free_planes(&f->gate_up);
-        free_planes(&f->down);
-        delete f;
+        destroy_ffn(f);
     }
     return HM_OK;
 }

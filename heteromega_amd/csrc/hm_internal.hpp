@@ -24,10 +24,17 @@ struct Planes {
 };
 
 // One source matrix of a repack: the reference tiles or logical tensors of a [K, N] matrix.
+// Column c of the source is packed column c + col_offset (col_mode 0), or, in a gate_up matrix interleaved per 64
+// channels (the reference's GateUpLayout::kInterleaved, kernels/gpu/include/heteromega/gpu_ffn.hpp:43-46), the gate
+// column (c / 64) * 128 + c % 64 (col_mode 1) or the up column 64 more (col_mode 2).
 struct TileSource {
     const uint8_t *tiles = nullptr;
     int64_t tiles_k = 0, tiles_n = 0; // of the whole packed matrix
+    int64_t col_offset = 0;
+    int col_mode = 0;
 };
+// Largest zero point the repack accepts (GPTQ checkpoints store z - 1, so z reaches 16 after adding the one back).
+constexpr uint32_t kMaxZero = 16;
 struct LogicalSource {
     const uint8_t *q = nullptr;      // [K, ld] row-major
     const uint16_t *scales = nullptr; // [K/group, ld]
@@ -36,12 +43,16 @@ struct LogicalSource {
 };
 
 // Repack launches. `fused` interleaves two sources per 16 columns (strip 2j from src[0], 2j + 1 from src[1]);
-// then N counts the columns of the result (2x the columns taken from each source).
+// then N counts the columns of the result (2x the columns taken from each source). A zero point above kMaxZero
+// sets bit 0 of *bad_zero (device memory, may be null).
 hipError_t launch_repack_tiles(const TileSource *src, int nsrc, bool fused, uint8_t *quant, uint32_t *meta, int64_t K,
-                               int64_t N, int dtype, hipStream_t stream);
+                               int64_t N, int dtype, uint32_t *bad_zero, hipStream_t stream);
 hipError_t launch_repack_logical(const LogicalSource *src, int nsrc, bool fused, uint8_t *quant, uint32_t *meta,
-                                 int64_t K, int64_t N, int64_t group, hipStream_t stream);
+                                 int64_t K, int64_t N, int64_t group, uint32_t *bad_zero, hipStream_t stream);
 hipError_t launch_unpack(const Planes &p, uint8_t *q, uint16_t *scales, uint8_t *zeros, hipStream_t stream);
+// Dequantized weights round((q - z) s) in the activation type: [N, K] (transposed, the orientation of the
+// reference's dequantize_packed) or [K, N], leading dimension ld.
+hipError_t launch_dequantize(const Planes &p, uint16_t *out, int64_t ld, bool transposed, hipStream_t stream);
 
 // Decode GEMV (M <= 16) on strips [strip_begin, strip_begin + n/16) and K tiles [kt_begin, kt_begin + kt_count).
 // fused: pairs of strips (gate, up) -> act = SiLU(gate) * up, n = output channels.

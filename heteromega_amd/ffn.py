@@ -44,6 +44,14 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
+def _layout(layout):
+    """GateUpLayout (gpu_ffn.hpp:43-46) by name."""
+    try:
+        return {"blocked": _lib.HM_GATE_UP_BLOCKED, "interleaved": _lib.HM_GATE_UP_INTERLEAVED}[layout]
+    except KeyError:
+        raise ValueError(f"gate_up layout must be 'blocked' or 'interleaved', got {layout!r}") from None
+
+
 def _call(status):
     if status == _lib.HM_INVALID_ARGUMENT:
         raise ValueError(_lib.last_error())
@@ -153,6 +161,7 @@ class RepackedMatrix:
         K, N, G, D, B = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32(), ctypes.c_int64()
         check(_lib.load().hm_weights_info(handle, ctypes.byref(K), ctypes.byref(N), ctypes.byref(G), ctypes.byref(D), ctypes.byref(B)))
         self.k, self.n, self.group, self.dtype, self.device_bytes = K.value, N.value, G.value, _TORCH_DTYPES[D.value], B.value
+        self.fused = False  # a fused gate_up matrix (from_gate_up_tiles): n = 2 x channels
 
     @classmethod
     def from_tiles(cls, tiles, packed_k, packed_n, k=None, n=None, dtype=torch.bfloat16, stream=None):
@@ -179,6 +188,30 @@ class RepackedMatrix:
         _call(_lib.load().hm_weights_from_logical(_ptr(q), _ptr(scales), _ptr(zeros), k, n, group, _hm_dtype(dtype),
                                                   _stream(stream, q.device), ctypes.byref(h)))
         return cls(h, q.device)
+
+    @classmethod
+    def from_gate_up_tiles(cls, gate_up, packed_k, stored, k=None, channels=None, layout="interleaved", dtype=torch.bfloat16, stream=None):
+        """The reference's fused gate_up tensor, packed [packed_k, 2 * stored] in `layout` order ("interleaved": per 64
+        channels their gate columns then their up columns; "blocked": gate | up), as FfnSliceWeights.gate_up holds it
+        (gpu_ffn.hpp:43-71). The result serves packed_linear_swiglu over channels [0, channels)."""
+        k = packed_k if k is None else k
+        channels = stored if channels is None else channels
+        if not gate_up.is_cuda or gate_up.dtype != torch.uint8 or not gate_up.is_contiguous() or gate_up.numel() != packed_bytes(packed_k, 2 * stored):
+            raise ValueError(f"from_gate_up_tiles: expected contiguous device uint8 of {packed_bytes(packed_k, 2 * stored)} bytes")
+        h = ctypes.c_void_p()
+        _call(_lib.load().hm_weights_from_gate_up_tiles(_ptr(gate_up), packed_k, stored, k, channels, _layout(layout), _hm_dtype(dtype),
+                                                        _stream(stream, gate_up.device), ctypes.byref(h)))
+        m = cls(h, gate_up.device)
+        m.fused = True
+        return m
+
+    def dequantize(self, transposed=True, stream=None):
+        """round((q - z) * s) in the activation type: [N, K] (QuantizedLinearImpl::dequantize_packed's orientation,
+        unified_llm_w4a16.cpp:710-790) or [K, N]."""
+        shape = (self.n, self.k) if transposed else (self.k, self.n)
+        out = torch.empty(shape, dtype=self.dtype, device=self.device)
+        _call(_lib.load().hm_weights_dequantize(self._h, _ptr(out), out.stride(0), 1 if transposed else 0, _stream(stream, self.device)))
+        return out
 
     @classmethod
     def concat(cls, parts, stream=None):
@@ -279,6 +312,28 @@ def packed_linear_k_split(out, inp, w0, w1, k0=None, k1=None, n=None, stream=Non
     return out
 
 
+def packed_linear_swiglu(act, inp, w, k=None, channels=None, stream=None, workspace=None):
+    """act[M, e - b] = SiLU(inp @ Wg[:k, b:e]) * (inp @ Wu[:k, b:e]) on a fused gate_up matrix (from_gate_up_tiles):
+    hipkernels::w4a16_gemm_fused_packed_tiles with fuse_activation (w4a16_gemm_packed.cu:549-578), any M.
+    channels=(b, e), all by default."""
+    if not w.fused:
+        raise ValueError("packed_linear_swiglu: needs a fused gate_up matrix (RepackedMatrix.from_gate_up_tiles)")
+    k = w.k if k is None else k
+    b, e = (0, w.n // 2) if channels is None else channels
+    if inp.dim() != 2 or inp.size(1) < k or inp.stride(1) != 1:
+        raise ValueError(f"packed_linear_swiglu: input must be [M, >= {k}] with unit column stride")
+    m = inp.size(0)
+    if act.dim() != 2 or act.size(0) != m or act.size(1) < e - b or act.stride(1) != 1:
+        raise ValueError(f"packed_linear_swiglu: output must be [M, >= {e - b}]")
+    lib = _lib.load()
+    need = lib.hm_linear_swiglu_workspace_bytes(w._h, m, k, e - b)
+    if workspace is None:
+        workspace = _workspace(need, inp.device)
+    wp, wb = _aligned(workspace, need)
+    _call(lib.hm_linear_swiglu(w._h, _ptr(act), act.stride(0), _ptr(inp), inp.stride(0), m, k, b, e, wp, wb, _stream(stream, inp.device)))
+    return act
+
+
 def gemv_w4a16(out, x, w, k=None, n=None, col_begin=0, stream=None):
     """M = 1 (heteromega::gemv_w4a16, gpu_ffn.hpp:99-103)."""
     if x.dim() != 2 or x.size(0) != 1:
@@ -356,6 +411,22 @@ class FfnLayer:
         _call(_lib.load().hm_ffn_from_tiles_padded(_ptr(gate), _ptr(up), _ptr(down), hidden, inter, ph, pi, _hm_dtype(dtype),
                                                    _stream(stream, gate.device), ctypes.byref(h)))
         return cls(h, gate.device)
+
+    @classmethod
+    def from_gate_up_tiles(cls, gate_up, down, hidden, inter, stored=None, layout="interleaved", dtype=torch.bfloat16, stream=None):
+        """From the reference's fused-FFN tensors (FfnSliceWeights, gpu_ffn.hpp:55-71; gemm_w4a16_ffn's inputs):
+        gate_up packed [hidden, 2 * stored] in `layout` order and down packed [stored, hidden]; the layer is channels
+        [0, inter) of them (prefix)."""
+        stored = inter if stored is None else stored
+        for t, (k, n) in ((gate_up, (hidden, 2 * stored)), (down, (stored, hidden))):
+            if not t.is_cuda or t.dtype != torch.uint8 or not t.is_contiguous():
+                raise ValueError("from_gate_up_tiles: packed matrices must be contiguous device uint8 tensors")
+            if packed_bytes(k, n) < 0 or t.numel() != packed_bytes(k, n):
+                raise ValueError(f"from_gate_up_tiles: a packed [{k}, {n}] matrix has {packed_bytes(k, n)} bytes, got {t.numel()}")
+        h = ctypes.c_void_p()
+        _call(_lib.load().hm_ffn_from_gate_up_tiles(_ptr(gate_up), _ptr(down), hidden, inter, stored, _layout(layout), _hm_dtype(dtype),
+                                                    _stream(stream, gate_up.device), ctypes.byref(h)))
+        return cls(h, gate_up.device)
 
     @classmethod
     def from_logical(cls, gate, up, down, group, dtype=torch.bfloat16, stream=None):
@@ -581,6 +652,7 @@ class GpuFfnModel:
 
 __all__ = [
     "HMError", "kTileK", "kTileN", "kTileBytes", "padded_rows", "packed_bytes", "packed_tile_index", "pack_w4a16",
-    "awq_unpack_qweight", "awq_unpack_qzeros", "gptq_unpack_qweight", "gptq_unpack_qzeros", "RepackedMatrix", "packed_linear", "packed_linear_k_split", "gemv_w4a16", "gemm_w4a16", "silu_mul",
+    "awq_unpack_qweight", "awq_unpack_qzeros", "gptq_unpack_qweight", "gptq_unpack_qzeros", "RepackedMatrix", "packed_linear", "packed_linear_k_split",
+    "packed_linear_swiglu", "gemv_w4a16", "gemm_w4a16", "silu_mul",
     "rmsnorm", "residual_add2", "residual_rmsnorm", "FfnLayer", "FFNPartition", "ffn_partitioned", "ffn_row_split", "GpuFfnModel",
 ]

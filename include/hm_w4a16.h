@@ -116,6 +116,28 @@ hm_status hm_weights_from_tiles(const uint8_t *tiles, int64_t packed_k, int64_t 
 hm_status hm_weights_from_logical(const uint8_t *q, const uint16_t *scales, const uint8_t *zeros, int64_t K,
                                   int64_t N, int64_t group, hm_dtype dtype, void *stream, hm_weights **out);
 
+/* Zero points. The engine reads every zero point as an unsigned byte and accepts 0..16 (int4 zeros, and 1..16 for
+ * GPTQ checkpoints that store z - 1); the create calls above and below return HM_INVALID_ARGUMENT for any other
+ * value, after waiting for the repack on `stream` (they are load-time calls). The reference's GPU GEMV reads tile
+ * zeros as int8 (src/hipkernels/w4a16_gemv_packed.cu:86-87), its CPU GEMV as uint8
+ * (src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:122-124); both agree with this on 0..16. */
+
+/* A gate_up matrix as the reference stores it for the fused FFN: packed [packed_k, 2 stored] with the gate and up
+ * columns of `stored` channels in `layout` order (HM_GATE_UP_INTERLEAVED: per 64 channels 64 gate columns then 64
+ * up columns; HM_GATE_UP_BLOCKED: all gate columns, then all up columns), kernels/gpu/include/heteromega/
+ * gpu_ffn.hpp:43-71 (FfnSliceWeights.gate_up), as read by the FUSE_ACT GEMM (src/hipkernels/w4a16_gemm_packed.cu:
+ * 549-578). The result is the fused gate_up of channels [0, channels) over the leading K rows (K % 128 == 0,
+ * channels % 16 == 0, channels <= stored, stored % 64 == 0); it runs through hm_linear_swiglu, not hm_linear. */
+hm_status hm_weights_from_gate_up_tiles(const uint8_t *gate_up, int64_t packed_k, int64_t stored, int64_t K, int64_t channels,
+                                        int32_t layout, hm_dtype dtype, void *stream, hm_weights **out);
+
+/* The dequantized weights round((q - z) * s) in the activation type (one rounding of the exact product), as
+ * QuantizedLinearImpl::dequantize_packed returns them (src/unified_llm_w4a16_hetero/unified_llm_w4a16.cpp:710-790):
+ * transposed != 0 writes [N, K] (the reference's [out, in] orientation, its transpose at :789), else [K, N]; ld_out is
+ * the leading dimension of `out` (transposed: a multiple of 8, 16-byte aligned). A fused gate_up matrix comes out
+ * with its columns alternating gate / up per 16 channels. */
+hm_status hm_weights_dequantize(const hm_weights *w, void *out, int64_t ld_out, int32_t transposed, void *stream);
+
 /* Writes the logical tensors back (device pointers, same shapes as above).
  * Round trip from_logical -> to_logical is bit-exact. */
 hm_status hm_weights_to_logical(const hm_weights *w, uint8_t *q, uint16_t *scales, uint8_t *zeros, void *stream);
@@ -151,6 +173,15 @@ hm_status hm_weights_concat(const hm_weights *const *parts, int32_t count, void 
 size_t hm_linear_workspace_bytes(const hm_weights *w, int64_t M, int64_t k, int64_t n);
 hm_status hm_linear(const hm_weights *w, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t M, int64_t k,
                     int64_t n, int64_t col_begin, void *workspace, size_t workspace_bytes, void *stream);
+
+/* SwiGLU projection on a fused gate_up matrix (hm_weights_from_gate_up_tiles):
+ *   act[M, ch_end - ch_begin] = SiLU(x[M, k] Wg[:k, ch]) * (x Wu[:k, ch]), fp32 sums, one rounding.
+ * Replaces hipkernels::w4a16_gemm_fused_packed_tiles with fuse_activation = true
+ * (include/hipkernels/w4a16_gemm_packed.hpp:41-49, src/hipkernels/w4a16_gemm_packed.cu:549-578, which rounds gate and
+ * up to bf16 first). Channels are multiples of 16 (M <= 16) or of 64 (M > 16). */
+size_t hm_linear_swiglu_workspace_bytes(const hm_weights *w, int64_t M, int64_t k, int64_t channels);
+hm_status hm_linear_swiglu(const hm_weights *w, void *act, int64_t ld_act, const void *x, int64_t ldx, int64_t M, int64_t k, int64_t ch_begin,
+                           int64_t ch_end, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
  * K split of one projection over two packed matrices (the pre-saved K-split
@@ -194,6 +225,14 @@ hm_status hm_ffn_from_tiles(const uint8_t *gate, const uint8_t *up, const uint8_
 hm_status hm_ffn_from_tiles_padded(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t hidden,
                                    int64_t inter, int64_t packed_hidden, int64_t packed_inter, hm_dtype dtype,
                                    void *stream, hm_ffn **out);
+
+/* From the reference's fused-FFN tensors: gate_up packed [hidden, 2 stored] in `layout` order (see
+ * hm_weights_from_gate_up_tiles) and down packed [stored, hidden]; the layer is channels [0, inter) of them
+ * (inter % 128 == 0, inter <= stored: the reference's FfnSliceWeights with its prefix(),
+ * kernels/gpu/include/heteromega/gpu_ffn.hpp:55-71, and the inputs of heteromega::gemm_w4a16_ffn,
+ * kernels/gpu/src/gemm_w4a16.cu:463-502). */
+hm_status hm_ffn_from_gate_up_tiles(const uint8_t *gate_up, const uint8_t *down, int64_t hidden, int64_t inter, int64_t stored,
+                                    int32_t layout, hm_dtype dtype, void *stream, hm_ffn **out);
 
 /* From logical device tensors (see hm_weights_from_logical), any group in {32, 64, 128}:
  * gate/up q [H, I], s/z [H/group, I]; down q [I, H], s/z [I/group, H]. */

@@ -179,6 +179,21 @@ def pack_tiles(q, s_bits, z):
     return out
 
 
+def join_gate_up(gate, up, layout):
+    """Logical gate and up (q, s, z) of n channels joined into one [rows, 2n] matrix in the reference's column order
+    (pack_ffn_slice, kernels/gpu/src/pack_w4a16.cpp:80-88): "blocked" = [gate | up], "interleaved" = per 64
+    channels their 64 gate columns, then their 64 up columns."""
+    out = []
+    for g, u in zip(gate, up):
+        g, u = np.asarray(g), np.asarray(u)
+        if layout == "blocked":
+            out.append(np.concatenate([g, u], axis=1))
+        else:
+            r, n = g.shape
+            out.append(np.stack([g.reshape(r, n // TILE_N, TILE_N), u.reshape(r, n // TILE_N, TILE_N)], axis=2).reshape(r, 2 * n))
+    return tuple(out)
+
+
 def pack_tiles_literal(q, s_bits, z):
     """numpy restatement of the model's tensor-op packer _pack_weights_packed without padding
     (py/unified_llm_w4a16/llama3_8b_w4a16_model.py:546-656 and unified_llm_w4a16.cpp:1242-1387): tiles by

@@ -120,3 +120,42 @@ def test_product_does_not_import_oracle():
             if f.endswith((".py", ".cpp", ".hip", ".hpp", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in text.replace("oracle/_ref", ""), f
+
+
+def test_pack_w4a16_rejects_zero_points_outside_range(hm):
+    import ctypes
+
+    import numpy as np
+
+    lib = hm._lib.load()
+    k, n = 128, 64
+    q = np.zeros((k, n), np.uint8)
+    s = np.full((1, n), 0x3C00, np.uint16)
+    out = np.empty(hm.packed_bytes(k, n), np.uint8)
+    for zv, ok in ((16, True), (17, False), (-1, False), (0, True)):
+        z = np.zeros((1, n), np.int8)
+        z[0, 7] = zv
+        st = lib.hm_pack_w4a16(q.ctypes.data_as(ctypes.c_void_p), s.ctypes.data_as(ctypes.c_void_p), z.ctypes.data_as(ctypes.c_void_p), k, n,
+                               out.ctypes.data_as(ctypes.c_void_p))
+        assert (st == hm._lib.HM_OK) == ok, (zv, st)
+        if not ok:
+            assert "zero point" in hm._lib.last_error()
+
+
+def test_reference_shim_loads_and_checks_arguments(hm):
+    # The reference-signature C++ operators compile against torch's headers and load; argument errors are torch
+    # errors before anything touches a GPU.
+    import torch
+
+    from heteromega_amd import _reference_shim as shim
+
+    for name in ("w4a16_gemm_fused_packed", "w4a16_gemm_fused_packed_tiles", "w4a16_gemv_fused_packed", "gemv_w4a16", "gemm_w4a16",
+                 "gemm_w4a16_ffn", "silu_mul", "packed_linear", "gpu_ffn_slice_forward", "GpuFfnModel"):
+        assert hasattr(shim, name), name
+    assert shim.gemm_w4a16_supports(17, 4096, 14336) and not shim.gemm_w4a16_supports(17, 4096, 100)
+    assert shim.gemm_w4a16_ffn_supports(1, 4096, 14336) and not shim.gemm_w4a16_ffn_supports(1, 4000, 14336)
+    x = torch.zeros((1, 128), dtype=torch.bfloat16)
+    out = torch.zeros((1, 64), dtype=torch.bfloat16)
+    packed = torch.zeros(4352, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="device uint8"):
+        shim.w4a16_gemv_fused_packed(out, x, packed, 128, 64, -1, 0, 0)
