@@ -587,20 +587,27 @@ void or_hm_gemv_emul(const uint16_t *x_bf16, const uint8_t *q, const uint16_t *s
 void or_hm_gemm_emul(const uint16_t *x_bf16, const uint8_t *q, const uint16_t *s, const uint8_t *z, int64_t M, int64_t K, int64_t N,
                      int64_t group, float *out, int threads) {
     if (threads < 1) threads = 1;
-#pragma omp parallel for schedule(static) num_threads(threads)
-    for (int64_t n = 0; n < N; ++n) {
-        for (int64_t m = 0; m < M; ++m) {
-            float acc = 0.0f;
+#pragma omp parallel num_threads(threads)
+    {
+        float *acc = (float *)malloc(sizeof(float) * (size_t)M);
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < N; ++n) {
+            for (int64_t m = 0; m < M; ++m) acc[m] = 0.0f;
             for (int64_t k0 = 0; k0 < K; k0 += 16) {
-                double step = 0.0;
-                for (int64_t k = k0; k < k0 + 16; ++k) {
+                double wv[16];
+                for (int j = 0; j < 16; ++j) {
+                    const int64_t k = k0 + j;
                     const float sc = or_bf16_to_f32(s[(k / group) * N + n]);
-                    const float wv = or_bf16_to_f32(or_bf16_from_f32((float)((int)q[k * N + n] - (int)z[(k / group) * N + n]) * sc));
-                    step += (double)wv * (double)or_bf16_to_f32(x_bf16[m * K + k]);
+                    wv[j] = (double)or_bf16_to_f32(or_bf16_from_f32((float)((int)q[k * N + n] - (int)z[(k / group) * N + n]) * sc));
                 }
-                acc = (float)((double)acc + step);
+                for (int64_t m = 0; m < M; ++m) {
+                    double step = 0.0;
+                    for (int j = 0; j < 16; ++j) step += wv[j] * (double)or_bf16_to_f32(x_bf16[m * K + k0 + j]);
+                    acc[m] = (float)((double)acc[m] + step);
+                }
             }
-            out[m * N + n] = acc;
+            for (int64_t m = 0; m < M; ++m) out[m * N + n] = acc[m];
         }
+        free(acc);
     }
 }
