@@ -11,5 +11,6 @@ _lib.load()
 
 from .ffn import *  # noqa: E402,F401,F403
 from .ffn import __all__ as _ffn_all  # noqa: E402
+from . import hetero  # noqa: E402,F401
 
-__all__ = list(_ffn_all)
+__all__ = list(_ffn_all) + ["hetero"]

@@ -90,6 +90,19 @@ _SIGNATURES = {
     "hm_residual_rmsnorm": (ctypes.c_int, [P, I64, P, I64, P, P, I64, I64, I64, ctypes.c_float, ctypes.c_int, P]),
     "hm_partition_check": (ctypes.c_int, [I64, I64, I64]),
     "hm_partition_from_ratio": (ctypes.c_int, [I64, ctypes.c_double, I64, ctypes.POINTER(I64)]),
+    "hm_split_type": (I32, [I32, I32, I32, I32, I32, I32]),
+    "hm_layer_id": (I32, [ctypes.c_char_p]),
+    "hm_split_table_create": (ctypes.c_int, [ctypes.POINTER(P)]),
+    "hm_split_table_destroy": (ctypes.c_int, [P]),
+    "hm_split_table_add_gemm": (ctypes.c_int, [P, I32, I32, I32, I32, I32, I32, I32, I32, I32, ctypes.POINTER(I32)]),
+    "hm_split_table_add_gemv": (ctypes.c_int, [P, I32, I32, I32, I32, I32, I32, I32, I32]),
+    "hm_split_table_find": (ctypes.c_int, [P, I32, I32, I32, I32, I32, P]),
+    "hm_split_table_size": (I64, [P]),
+    "hm_linear_split_workspace_bytes": (SZ, [P, P, P, I64, I64, I64]),
+    "hm_linear_split": (ctypes.c_int, [P, P, P, P, I64, P, I64, I64, I64, I64, P, SZ, P]),
+    "hm_merged_ffn_check": (ctypes.c_int, [I64, I64, I64, I64, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.POINTER(ctypes.c_uint64)]),
+    "hm_merged_ffn_supports": (I32, [I64, I64, I64, I64, I64, I64]),
 }
 
 _lib = None

@@ -16,7 +16,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libhmw4a16.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["hm_api.cpp", "hm_layout.hip", "hm_gemv.hip", "hm_gemm.hip", "hm_elementwise.hip", "hm_static.hip"]
+SOURCES = ["hm_api.cpp", "hm_split.cpp", "hm_layout.hip", "hm_gemv.hip", "hm_gemm.hip", "hm_elementwise.hip", "hm_static.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

@@ -324,6 +324,72 @@ hm_status hm_partition_check(int64_t intermediate, int64_t npu_channels, int64_t
  * (FFNPartition.from_ratio, reference.py:135-144). */
 hm_status hm_partition_from_ratio(int64_t intermediate, double npu_ratio, int64_t alignment, int64_t *npu_channels);
 
+/* ---------------------------------------------------------------------------
+ * Split descriptors of the reference's hetero executor (host, no GPU needed to plan).
+ * A projection's config entry is keyed by {forM, forK, forN, layer_id, chunk_id} (NPUKey) and holds the other
+ * device's shares {npuM, npuK, npuN, cpuN, cpuThreads, config} plus a split_type derived from the shapes
+ * (NPUValue; include/unified_llm_w4a16_hetero/npuSetup.hpp:93-109). On this build every share runs on the GPU:
+ * hm_linear_split executes the split an entry describes as GPU launches, so a config table written for the
+ * reference drives the same partition here.
+ * ------------------------------------------------------------------------- */
+typedef struct hm_split_desc {
+    int32_t hw_idx, inst_idx; /* the other device's contexts in the reference; unused here (-1) */
+    int32_t npuM, npuK, npuN, cpuN, cpuThreads, config;
+    int32_t split_type; /* > 0: K split at K0 = split_type; -1: M split; -2: N split; 0: GEMV column shares */
+} hm_split_desc;
+
+/* split_type of a kernel config (src/unified_llm_w4a16_hetero/npuSetup.cpp:1283-1291): npuK when forK != npuK
+ * (a K split, taking precedence), -1 when only M differs, -2 when N differs, -1 otherwise. */
+int32_t hm_split_type(int32_t forM, int32_t forK, int32_t forN, int32_t npuM, int32_t npuK, int32_t npuN);
+
+/* layer_id of a layer name: qkv 8, q 1, k 2, v 3, o 4, gate 5, up 6, down 7, anything else 0
+ * (get_layer_id, npuSetup.cpp:635-653). */
+int32_t hm_layer_id(const char *layer_type);
+
+typedef struct hm_split_table hm_split_table; /* config_map (npuSetup.hpp:114) */
+hm_status hm_split_table_create(hm_split_table **out);
+hm_status hm_split_table_destroy(hm_split_table *t);
+/* A GEMM entry as the config loader makes it (npuSetup.cpp:1283-1467): split_type by hm_split_type, cpuN 0,
+ * cpuThreads 1. Rejected: negative or zero sizes, npuK > forK (a K share past the projection), K splits whose shares
+ * are not multiples of 128. Entries with npuM == 0 are GPU-only in the reference and are not stored (returns HM_OK
+ * and *stored = 0). */
+hm_status hm_split_table_add_gemm(hm_split_table *t, int32_t forM, int32_t forK, int32_t forN, int32_t layer_id, int32_t chunk_id,
+                                  int32_t npuM, int32_t npuK, int32_t npuN, int32_t config, int32_t *stored);
+/* A GEMV entry (M = 1) with column shares (npuSetup.cpp:1763: {-1, -1, npuM, npuK, 0, cpuN, threads, config, 0}). */
+hm_status hm_split_table_add_gemv(hm_split_table *t, int32_t forK, int32_t forN, int32_t layer_id, int32_t chunk_id, int32_t npuN, int32_t cpuN,
+                                  int32_t cpuThreads, int32_t config);
+/* Exact-key lookup (find_config_entry, src/unified_llm_w4a16_hetero/hetero_compute.cpp:98-106): HM_OK and *out, or
+ * HM_INVALID_ARGUMENT when no entry has this key (chunk -1 is not a wildcard). */
+hm_status hm_split_table_find(const hm_split_table *t, int32_t M, int32_t K, int32_t N, int32_t layer_id, int32_t chunk_id, hm_split_desc *out);
+int64_t hm_split_table_size(const hm_split_table *t);
+
+/* y [M, N] = x [M, K] @ W, split as `d` describes, every share on the GPU, in the order the reference launches them:
+ *   d NULL: one launch (the reference's GPU default path).
+ *   split_type > 0 (K split, hetero_matmul_out_gem{m,v}_packed_K, hetero_compute.cpp:282-447, 633-805): w0 holds rows
+ *     [0, K0) and w1 rows [K0, K) with K0 = split_type; y = round(round(x0 W0) + round(x1 W1)) (hm_linear_k_split).
+ *   M == 1 otherwise (hetero_matmul_out_gemv_packed_M, :497-560): columns [0, npuN), [npuN, npuN + cpuN) and the rest,
+ *     with both shares dropped when npuN + cpuN > N and cpuN dropped unless a multiple of 64, as the reference does.
+ *     (The reference sizes the GPU's columns before it drops such a cpuN, :516-538, and leaves those columns
+ *     unwritten; here the GPU's share covers them.)
+ *   split_type -1 (M split, :189-259): rows [0, M - npuM) and [M - npuM, M) (npuM clamped to M).
+ *   split_type -2 (N split): columns [0, npuN) and [npuN, N).
+ * Column and row shares of one projection give the bits of the unsplit launch where the launches do not split K
+ * differently (the GEMM splits K only for grids under two workgroups per CU). */
+size_t hm_linear_split_workspace_bytes(const hm_split_desc *d, const hm_weights *w0, const hm_weights *w1, int64_t M, int64_t K, int64_t N);
+hm_status hm_linear_split(const hm_split_desc *d, const hm_weights *w0, const hm_weights *w1, void *y, int64_t ldy, const void *x, int64_t ldx,
+                          int64_t M, int64_t K, int64_t N, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The merged-FFN deployment contract's shape and partition rules (MergedFfnConfig::load and its buffer sizes,
+ * include/heteromega/merged_ffn_contract.hpp:41-127): m a positive multiple of 512, hidden and intermediate of 128,
+ * npu_channels a positive multiple of 256 below intermediate and at most 8192. Sizes: activations m * hidden * 2,
+ * intermediate m * npu_channels * 2, weights (hidden / 128) * (intermediate / 64) * 4352 bytes, each product checked
+ * for overflow (checked_product). The artifact fields (xclbin hashes, layouts, fifo depths) describe NPU binaries and
+ * have no counterpart here. */
+hm_status hm_merged_ffn_check(int64_t m, int64_t hidden, int64_t intermediate, int64_t npu_channels, uint64_t *activation_bytes,
+                              uint64_t *intermediate_bytes, uint64_t *weight_bytes);
+/* MergedFfnConfig::supports: rows > 1 and the exact shape of the contract. */
+int32_t hm_merged_ffn_supports(int64_t m, int64_t hidden, int64_t intermediate, int64_t rows, int64_t h, int64_t inter);
+
 #ifdef __cplusplus
 }
 #endif
