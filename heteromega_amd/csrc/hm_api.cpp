@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 struct hm_weights {
@@ -25,6 +26,7 @@ struct hm_ffn {
     hm_weights gate_up; // [H, 2 I], strips alternate gate / up per 16 channels
     hm_weights down;    // [I, H]
     int64_t hidden = 0, inter = 0;
+    size_t decode_partial[17] = {}; // largest split-partial buffer of any call of 1..m rows (m <= 16), planned at creation
 };
 
 namespace {
@@ -338,6 +340,11 @@ template <class Launches> hm_status fill_ffn(hm_ffn *f, hipStream_t s, const cha
         destroy_ffn(f);
         return st;
     }
+    for (int64_t m = 1; m <= kGemvMaxRows; ++m) {
+        const size_t d = linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false);
+        const size_t g = linear_workspace(f->gate_up.p, m, f->inter, f->hidden / 128, true);
+        f->decode_partial[m] = std::max({f->decode_partial[m - 1], d, g});
+    }
     *out = f;
     return HM_OK;
 }
@@ -367,6 +374,31 @@ hm_status build_ffn_from_tiles(const hm::TileSource gu[2], const uint8_t *down, 
 }
 
 } // namespace
+
+hm::Topology hm::device_topology() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static Topology cache[kMaxDevices];
+    static bool known[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        return Topology{};
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!known[dev]) {
+        Topology t;
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) {
+            t.cus = v;
+        }
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0) {
+            t.xcds = v;
+        }
+        cache[dev] = t;
+        known[dev] = true;
+    }
+    return cache[dev];
+}
 
 hm_status hm::set_error(hm_status s, const char *fmt, ...) {
     va_list ap;
@@ -912,15 +944,12 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
         return 0;
     }
     const size_t act = static_cast<size_t>(round_up(max_m * f->inter * 2, 256));
-    // The largest partial buffer of any M up to max_m and any channel range: the GEMV's (M <= 16) and, above,
-    // the GEMM's small-grid K split, which never needs more than kGemmPartialMax.
-    size_t partial = max_m > kGemvMaxRows ? hm::kGemmPartialMax : 0;
-    for (int64_t m = 1; m <= std::min<int64_t>(max_m, kGemvMaxRows); ++m) {
-        const size_t d = linear_workspace(f->down.p, m, f->hidden, f->inter / 128, false);
-        const size_t g = linear_workspace(f->gate_up.p, m, f->inter, f->hidden / 128, true);
-        partial = std::max(partial, std::max(d, g));
+    // The largest partial buffer of any M up to max_m and any channel range: the GEMV's (M <= 16, planned when the
+    // layer was made) and, above, the GEMM's small-grid K split, which never needs more than kGemmPartialMax.
+    if (max_m <= kGemvMaxRows) {
+        return act + f->decode_partial[max_m];
     }
-    return act + partial;
+    return act + std::max(hm::kGemmPartialMax, f->decode_partial[kGemvMaxRows]);
 }
 
 hm_status hm_ffn_gate_up(const hm_ffn *f, void *act, int64_t ld_act, const void *x, int64_t ldx, int64_t M, int64_t ch_begin, int64_t ch_end,

@@ -20,7 +20,7 @@
 // at the start of K tile kt (DEPTH 2, or 4 for the 64-row tiles, whose small grids expose each workgroup's own
 // latency).
 //
-// Tiles are dealt to XCDs in contiguous runs (workgroup i runs on XCD i % 8) of an order that walks bands of 4
+// Tiles are dealt to XCDs in contiguous runs (workgroup i runs on XCD i % 8 on an MI355X) of an order that walks bands of 4
 // row tiles column by column, so the workgroups resident on one XCD share both activation rows and weight
 // columns in its L2.
 //
@@ -57,6 +57,7 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     int accumulate; // plain output: y = round(y + round(sum)) instead of y = round(sum)
     int group_m;    // tile order: bands of group_m row tiles, column-major inside a band (1: row-major)
+    int xcds;       // XCDs of the device: the dispatcher places workgroup i on XCD i % xcds
 };
 
 // Per (strip, group) dequantization constants, made once per K tile from the scale/zero record.
@@ -176,12 +177,12 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     const int col = lane & 15;
     const int h = lane >> 4;
 
-    // Workgroup -> tile: XCD x = blockIdx.x % 8 takes a contiguous run of the tile order (row-major, or bands of
-    // group_m row tiles walked column by column).
+    // Workgroup -> tile: XCD x = blockIdx.x % xcds takes a contiguous run of the tile order (row-major, or bands
+    // of group_m row tiles walked column by column).
     const int nt = a.tiles_m * a.tiles_n;
-    const int q8 = nt / 8, r8 = nt % 8;
-    const int xcd = static_cast<int>(blockIdx.x) % 8;
-    const int lin = xcd * q8 + min(xcd, r8) + static_cast<int>(blockIdx.x) / 8;
+    const int qx = nt / a.xcds, rx = nt % a.xcds;
+    const int xcd = static_cast<int>(blockIdx.x) % a.xcds;
+    const int lin = xcd * qx + min(xcd, rx) + static_cast<int>(blockIdx.x) / a.xcds;
     int tm, tn;
     if (a.group_m > 1) {
         const int band_tiles = a.group_m * a.tiles_n;
@@ -459,12 +460,11 @@ template <class T> hipError_t launch_t(const GemmArgs &a, int group, bool fused,
     }
 }
 
-constexpr int kCUs = 256;
-
 } // namespace
 
 GemmPlan plan_gemm(const GemmCall &c) {
     GemmPlan p;
+    const int64_t cus = device_topology().cus;
     const int64_t cols = c.fused ? 2 * c.n : c.n;
     const int64_t rows128 = (c.m + 127) / 128;
     // 128 x 128 tiles from 160 of them (5/8 of the CUs: measured on the Llama-3-8B and Qwen2.5-14B projections
@@ -474,19 +474,13 @@ GemmPlan plan_gemm(const GemmCall &c) {
     // 2-34% slower for one to six partial rounds and for small grids, where the 4-wave tiles balance better.
     // All three accumulate every output element in the same order, so without a K split a row block computed
     // alone gives the same bits as inside a larger call.
-    p.cfg = rows128 * (cols / 128) >= 5 * kCUs / 8 ? 1 : 0;
+    p.cfg = rows128 * (cols / 128) >= 5 * cus / 8 ? 1 : 0;
     const int64_t wide = cols % 256 == 0 ? rows128 * (cols / 256) : 0;
     // A fused gate_up of 1.5 to 2 rounds of 128 x 256 tiles takes them too (the layer at M = 512: Llama-3-8B
     // -3.6%, Qwen2.5-14B -4.6%, bf16 -2.7%); the long-K down projections at such grids stay at 128 x 128
     // (15% slower otherwise).
-    if (p.cfg == 1 && ((wide >= 5 * kCUs / 8 && wide <= kCUs) || wide >= 6 * kCUs || (c.fused && wide >= 3 * kCUs / 2 && wide < 2 * kCUs))) {
+    if (p.cfg == 1 && ((wide >= 5 * cus / 8 && wide <= cus) || wide >= 6 * cus || (c.fused && wide >= 3 * cus / 2 && wide < 2 * cus))) {
         p.cfg = 2;
-    }
-    // Tuning overrides, read once per process (the workspace query plans every column width).
-    static const int env_cfg = std::getenv("HM_GEMM_CFG") != nullptr ? std::atoi(std::getenv("HM_GEMM_CFG")) : -1;
-    static const bool env_nosplit = std::getenv("HM_GEMM_NOSPLIT") != nullptr;
-    if (env_cfg >= 0 && env_cfg <= 2 && (env_cfg < 2 || cols % 256 == 0)) {
-        p.cfg = env_cfg;
     }
     // Tile shape of each configuration; launch_g instantiates the kernel with the same shape.
     const int64_t bm = p.cfg >= 1 ? 128 : 64;
@@ -505,9 +499,9 @@ GemmPlan plan_gemm(const GemmCall &c) {
     // 32 K tiles in two (a 1024-column projection at M = 2048) slower. A row block's bits then depend on whether
     // its call splits (grids that do not split keep them).
     const int64_t wgs = p.tiles_m * p.tiles_n;
-    const bool small = wgs < kCUs / 2;
-    const int64_t aim = small ? kCUs : (p.cfg != 2 && wgs < 2 * kCUs ? 2 * kCUs : 0);
-    if (aim > 0 && c.kt_count >= 16 && !env_nosplit) {
+    const bool small = wgs < cus / 2;
+    const int64_t aim = small ? cus : (p.cfg != 2 && wgs < 2 * cus ? 2 * cus : 0);
+    if (aim > 0 && c.kt_count >= 16) {
         int64_t splits = std::min<int64_t>((aim + wgs - 1) / wgs, c.kt_count / (small ? 8 : 24));
         while (splits > 1 && static_cast<size_t>(splits) * c.m * cols * sizeof(float) > kGemmPartialMax) {
             --splits;
@@ -545,9 +539,9 @@ hipError_t launch_gemm(const GemmCall &c, hipStream_t stream) {
     // hold about 4 row blocks x 8 column blocks: 4 x 32 KiB of activations and 8 x 16 KiB of weights per K tile
     // through its L2, against 32 + 32 x 16 KiB in row-major order. Measured (same bits): Llama-3-8B layer at
     // M = 512 / 1024 / 2048 -2.2 / -1.7 / -1.7%, Qwen2.5-14B at M = 1024 / 2048 -1.7%; bands of 2 gained 1.2-1.4%,
-    // of 8 and 16 less or nothing. HM_GEMM_GROUP overrides (tuning; 1 is row-major).
-    static const int env_group = std::getenv("HM_GEMM_GROUP") != nullptr ? std::atoi(std::getenv("HM_GEMM_GROUP")) : 4;
-    a.group_m = std::max(env_group, 1);
+    // of 8 and 16 less or nothing.
+    a.group_m = 4;
+    a.xcds = device_topology().xcds;
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(p.splits));
     const int group = static_cast<int>(c.w.group);
     hipError_t e = c.w.dtype == 1 ? launch_t<F16>(a, group, c.fused, p.cfg, grid, stream)

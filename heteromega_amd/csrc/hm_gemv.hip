@@ -41,9 +41,10 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr size_t kXBudget = 64 * 1024;   // staged activation bytes per workgroup at one row (bounds a split's K range)
 constexpr size_t kStageMax = 144 * 1024; // staged activation bytes per workgroup at several rows (LDS is 160 KiB)
-constexpr int64_t kCUs = 256;            // compute units of an MI355X
-constexpr int64_t kUnits = 7 * kCUs / 2; // (strip group, split) units a launch with several rows aims for
 constexpr int kNormChunks = 4;           // RMSNorm in the staging: rows of up to 4 x 2048 columns
+
+// (strip group, split) units a launch with several rows aims for: 3.5 per CU.
+int64_t target_units(int64_t cus) { return 7 * cus / 2; }
 
 struct GemvArgs {
     const uint4 *quant;
@@ -583,15 +584,12 @@ hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, int spw, dim3 
     return a.m <= 1 ? launch_m<T, 1>(a, group, fused, spw, grid, waves, lds, s) : launch_m<T, 16>(a, group, fused, spw, grid, waves, lds, s);
 }
 
-int env_int(const char *name) {
-    const char *v = std::getenv(name);
-    return v != nullptr ? std::atoi(v) : 0;
-}
-
 } // namespace
 
 GemvPlan plan_gemv(const GemvCall &c) {
     GemvPlan p;
+    const int64_t cus = device_topology().cus;
+    const int64_t units = target_units(cus);
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
     p.spw = c.fused ? 2 : (c.m > 1 && strips % 2 == 0 ? 2 : 1);
     p.groups = strips / p.spw;
@@ -612,14 +610,10 @@ GemvPlan plan_gemv(const GemvCall &c) {
         // Several rows (launch shapes measured on the Llama-3-8B projections at M = 4 and 16, weights
         // streamed from HBM): narrow grids (under 1.75 strip groups per CU) are split along K until there are
         // 3.5 (strip group, split) units per CU; the staged chunk must leave room in LDS for the reduction.
-        set_splits(p.groups < kUnits / 2 ? (kUnits + p.groups - 1) / p.groups : 1);
+        set_splits(p.groups < units / 2 ? (units + p.groups - 1) / p.groups : 1);
         while (stage_bytes(p.kt_per_split) > kStageMax && p.kt_per_split > 1) {
             set_splits(p.splits + 1);
         }
-    }
-    if (const int kts = env_int("HM_GEMV_KTS")) { // tuning override: K tiles per split
-        p.kt_per_split = std::min<int64_t>(kts, c.kt_count);
-        p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
     }
     p.wps = 1;
     p.nu = 1;
@@ -636,7 +630,7 @@ GemvPlan plan_gemv(const GemvCall &c) {
         }
         // Between one and two strip groups per CU (Qwen2.5-14B down: 320 strips), workgroups of twice the strips
         // run one round on fewer CUs: measured 11.2 µs against 12.1 µs for 320 workgroups.
-        if (!c.fused && p.groups > kCUs && p.groups < 2 * kCUs && p.nu * p.wps <= 8) {
+        if (!c.fused && p.groups > cus && p.groups < 2 * cus && p.nu * p.wps <= 8) {
             p.nu *= 2;
         }
     } else {
@@ -655,15 +649,9 @@ GemvPlan plan_gemv(const GemvCall &c) {
         // From 8 rows, 16-wave workgroups share the chunk further while the grid keeps about one workgroup per
         // CU (measured: faster at 8 and 16 rows, slower at 4).
         const auto wgs = [&](int64_t nu) { return (p.groups + nu - 1) / nu * p.splits; };
-        while (c.m >= 8 && p.nu * p.wps < 16 && wgs(2 * p.nu) >= 27 * kCUs / 32) {
+        while (c.m >= 8 && p.nu * p.wps < 16 && wgs(2 * p.nu) >= 27 * cus / 32) {
             p.nu *= 2;
         }
-    }
-    if (const int nu = env_int("HM_GEMV_NU")) { // tuning override
-        p.nu = nu;
-    }
-    if (const int wps = env_int("HM_GEMV_WPS")) {
-        p.wps = wps;
     }
     p.waves = p.nu * p.wps;
     const int64_t kc = p.kt_per_split * 128;
@@ -676,10 +664,11 @@ GemvPlan plan_gemv(const GemvCall &c) {
 }
 
 size_t gemv_partial_bound(const GemvCall &c) {
-    // With several rows a range of fewer than kUnits / 2 strip groups takes ceil(kUnits / groups) splits,
-    // so splits * groups < 3 kUnits / 2; the staging-driven splits do not grow as the range narrows.
+    // With several rows a range of fewer than units / 2 strip groups takes ceil(units / groups) splits,
+    // so splits * groups < 3 units / 2; the staging-driven splits do not grow as the range narrows.
     const GemvPlan p = plan_gemv(c);
-    const size_t narrow = c.m > 1 ? static_cast<size_t>(3 * kUnits / 2) * p.spw * c.m * 16 * sizeof(float) : 0;
+    const int64_t units = target_units(device_topology().cus);
+    const size_t narrow = c.m > 1 ? static_cast<size_t>(3 * units / 2) * p.spw * c.m * 16 * sizeof(float) : 0;
     return std::max(p.partial_bytes, narrow);
 }
 

@@ -14,6 +14,14 @@ namespace hm {
 // Records the message of a failed C ABI call for hm_last_error() on this thread and returns s.
 hm_status set_error(hm_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// Compute units and XCDs of the current device (queried once per device; 256 and 8 on an MI355X). Launch planning
+// sizes grids by the CU count; the GEMM deals tiles to XCDs, onto which the dispatcher places workgroup i at i % xcds.
+struct Topology {
+    int64_t cus = 256;
+    int xcds = 8;
+};
+Topology device_topology();
+
 // Device planes of one repacked matrix (layout: hm_device.hpp).
 struct Planes {
     const uint8_t *quant = nullptr; // (N/16) * (K/128) KiB

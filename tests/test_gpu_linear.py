@@ -90,20 +90,22 @@ def test_linear_odd_strip_count(oracle, hm, device, group, m):
     assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, group, dtype), dtype, f"odd strips g={group} M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 3])
-def test_linear_waves_without_tiles(oracle, hm, device, monkeypatch, m):
-    # Forced launch shape (tuning overrides): 8 waves per strip over 3 K tiles leaves 5 waves with no tile;
-    # their zero-weighted steps must not leak anything (with M = 1 they read LDS no wave staged).
-    monkeypatch.setenv("HM_GEMV_NU", "1")
-    monkeypatch.setenv("HM_GEMV_WPS", "8")
-    rng = np.random.default_rng(700 + m)
-    k, n, dtype = 384, 64, "fp16"
-    w_np, w = _matrix(oracle, hm, rng, k, n, 128, dtype, device)
-    x64, x = make_x(oracle, rng, m, k, dtype, device)
-    y = torch.empty((m, n), dtype=torch.float16, device=device)
-    hm.packed_linear(y, x, w)
+@pytest.mark.parametrize("k1", [128, 256])
+def test_linear_waves_without_tiles(oracle, hm, device, k1):
+    # A K-split pair at one row runs both shares in one GEMV launch with the longer share's wave split: 8 waves per
+    # strip for the 64 K tiles of share 0, so the 1 or 2 K tiles of share 1 leave waves of its split with no tile.
+    # Their steps must not leak anything (they read LDS that no wave of their range staged).
+    rng = np.random.default_rng(700 + k1)
+    k0, n, dtype = 8192, 64, "fp16"
+    w0_np, w0 = _matrix(oracle, hm, rng, k0, n, 128, dtype, device)
+    w1_np, w1 = _matrix(oracle, hm, rng, k1, n, 128, dtype, device)
+    x64, x = make_x(oracle, rng, 1, k0 + k1, dtype, device)
+    y = torch.empty((1, n), dtype=torch.float16, device=device)
+    hm.packed_linear_k_split(y, x, w0, w1)
     torch.cuda.synchronize()
-    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, 128, dtype), dtype, f"idle waves M={m}")
+    a = oracle.round_to((x64[:, :k0] @ oracle.weights_f64(*w0_np, 128, dtype)).astype(np.float32), dtype)
+    b = oracle.round_to((x64[:, k0:] @ oracle.weights_f64(*w1_np, 128, dtype)).astype(np.float32), dtype)
+    assert_close(oracle, host_f64(y), a.astype(np.float64) + b, dtype, f"idle waves k1={k1}")
 
 
 def test_linear_split_k_path(oracle, hm, device):
