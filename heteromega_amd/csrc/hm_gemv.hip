@@ -11,9 +11,15 @@
 // Streaming. Each wave keeps a ring of KB steps (S strip tiles and their scale/zero records per step) in
 // flight: the tile of step i + KB is requested as soon as step i has consumed its registers, and each step
 // waits only for its own loads (in-order vmcnt). A strip tile is 1 KiB read with one 16-byte load per lane,
-// so every wave load is fully coalesced; weights use non-temporal loads. A ring of 8 tiles per wave keeps
-// the register count near 100, so four or more waves fit per SIMD and every workgroup of a decode launch is
-// resident at once (the launch streams without a second round of workgroups).
+// so every wave load is fully coalesced; weights use non-temporal loads. With several rows the ring holds 8
+// tiles (4 where the records or the four-row folds need the registers), which keeps the register count near
+// 100, so four or more waves fit per SIMD and every workgroup of a decode launch is resident at once (the
+// launch streams without a second round of workgroups). With one row the launch picks the ring depth (3, 4
+// or 8 steps; strip pairs at most 4) from its wave count so that about kRingSteps steps are in flight over
+// the whole launch: more than that only lengthens the memory queues and the launch's tail (measured on the
+// Llama-3-8B, Qwen2.5-14B and Llama-3.2-1B projections: down at 2048 waves 7.3 us with 4 steps against 7.6
+// with 8, at 2560 waves 9.8 us with 3 against 11.2 with 8, and at 1024 waves 4.6 us with 8 against 4.8
+// with 4).
 //
 // Math per strip tile (4 MFMA steps of 32 K): the B operand is bias + q straight from the nibbles
 // (hm_device.hpp), A is the activation rows from LDS, so
@@ -42,6 +48,11 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr size_t kXBudget = 64 * 1024;   // staged activation bytes per workgroup at one row (bounds a split's K range)
 constexpr size_t kStageMax = 144 * 1024; // staged activation bytes per workgroup at several rows (LDS is 160 KiB)
 constexpr int kNormChunks = 4;           // RMSNorm in the staging: rows of up to 4 x 2048 columns
+constexpr int64_t kRingSteps = 8192;     // ring steps in flight over a one-row launch (8 MiB of single-strip tiles)
+
+// Ring depth of a one-row launch of `waves` waves: the deepest of 8, 4 and 3 steps that keeps at most
+// kRingSteps steps in flight, and 3 beyond that.
+int ring_depth(int64_t waves) { return waves * 8 <= kRingSteps ? 8 : waves * 4 <= kRingSteps ? 4 : 3; }
 
 // (strip group, split) units a launch with several rows aims for: 3.5 per CU.
 int64_t target_units(int64_t cus) { return 7 * cus / 2; }
@@ -98,7 +109,9 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
 
 // Dynamic LDS: xs [m][kc + 8] 16-bit, sums [m][kc / G + 1] float2 (Xb, X); after the multiply the front of
 // the same space holds red [waves][S][m][16] float.
-template <class T, int MT, int G, int S, bool FUSED, int WGS>
+// RING: ring depth in steps for one row (MT == 1, group >= 64), at most 8 tiles; the other instantiations
+// size their ring themselves and take RING = 0.
+template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING>
 __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int ROWS = MT == 1 ? 1 : 4; // D elements per lane that can hold a real row
@@ -107,7 +120,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     // Ring depth in steps: 8 tiles in flight per wave, fewer where the records (group < 128) and the
     // four-row folds (M > 1) need the registers.
     constexpr int kInFlight = (MT > 1 && (S == 1 || GPT > 1)) ? 4 : 8; // strip tiles
-    constexpr int KB = kInFlight / S / (GPT == 4 ? 2 : 1) > 0 ? kInFlight / S / (GPT == 4 ? 2 : 1) : 1;
+    constexpr int KB_SIZED = kInFlight / S / (GPT == 4 ? 2 : 1) > 0 ? kInFlight / S / (GPT == 4 ? 2 : 1) : 1;
+    constexpr int KB = RING > 0 ? RING : KB_SIZED;
+    static_assert(RING == 0 || (MT == 1 && GPT < 4 && S * RING <= 8), "a chosen ring depth is for one row, groups of 64 or 128, at most 8 tiles");
     constexpr int CPG = G / 8;             // 8-element activation chunks per group
     constexpr int kPre = 4;                // chunks per thread fetched ahead of the weights
 
@@ -530,9 +545,9 @@ __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ part
     y[row * ldy + c] = accumulate ? T::from_float(T::to_float(y[row * ldy + c]) + T::to_float(out)) : out;
 }
 
-template <class T, int MT, int G, int S, bool FUSED, int WGS>
+template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING>
 hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
-    auto kern = gemv_kernel<T, MT, G, S, FUSED, WGS>;
+    auto kern = gemv_kernel<T, MT, G, S, FUSED, WGS, RING>;
     // One attribute call per instantiation; a function-local static is initialized once even when several
     // host threads launch at the same time.
     static const hipError_t configured =
@@ -544,44 +559,64 @@ hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <class T, int MT, int G, int S, bool FUSED, int WGS>
+hipError_t launch_r(const GemvArgs &a, dim3 grid, int ring, size_t lds, hipStream_t s) {
+    if constexpr (MT == 1 && G != 32) {
+        // Strip pairs stop at 4 steps (8 tiles): measured slower with 8 (Llama-3.2-1B gate_up at 512 waves:
+        // 7.2 us against 6.6).
+        constexpr int deep = S == 2 ? 4 : 8;
+        switch (ring) {
+        case 3:
+            return launch_w<T, MT, G, S, FUSED, WGS, 3>(a, grid, lds, s);
+        case 8:
+            return launch_w<T, MT, G, S, FUSED, WGS, deep>(a, grid, lds, s);
+        default:
+            return launch_w<T, MT, G, S, FUSED, WGS, 4>(a, grid, lds, s);
+        }
+    } else {
+        return launch_w<T, MT, G, S, FUSED, WGS, 0>(a, grid, lds, s);
+    }
+}
+
 template <class T, int MT, int G, int S, bool FUSED>
-hipError_t launch_s(const GemvArgs &a, dim3 grid, int waves, size_t lds, hipStream_t s) {
+hipError_t launch_s(const GemvArgs &a, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
     switch (waves) {
     case 4:
-        return launch_w<T, MT, G, S, FUSED, 256>(a, grid, lds, s);
+        return launch_r<T, MT, G, S, FUSED, 256>(a, grid, ring, lds, s);
     case 8:
-        return launch_w<T, MT, G, S, FUSED, 512>(a, grid, lds, s);
+        return launch_r<T, MT, G, S, FUSED, 512>(a, grid, ring, lds, s);
     default:
-        return launch_w<T, MT, G, S, FUSED, 1024>(a, grid, lds, s);
+        return launch_r<T, MT, G, S, FUSED, 1024>(a, grid, ring, lds, s);
     }
 }
 
 template <class T, int MT, int G>
-hipError_t launch_g(const GemvArgs &a, bool fused, int strips_per_wave, dim3 grid, int waves, size_t lds, hipStream_t s) {
+hipError_t launch_g(const GemvArgs &a, bool fused, int strips_per_wave, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
     if (fused) {
-        return launch_s<T, MT, G, 2, true>(a, grid, waves, lds, s);
+        return launch_s<T, MT, G, 2, true>(a, grid, waves, ring, lds, s);
     }
     if (strips_per_wave == 2) {
-        return launch_s<T, MT, G, 2, false>(a, grid, waves, lds, s);
+        return launch_s<T, MT, G, 2, false>(a, grid, waves, ring, lds, s);
     }
-    return launch_s<T, MT, G, 1, false>(a, grid, waves, lds, s);
+    return launch_s<T, MT, G, 1, false>(a, grid, waves, ring, lds, s);
 }
 
 template <class T, int MT>
-hipError_t launch_m(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, size_t lds, hipStream_t s) {
+hipError_t launch_m(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
     switch (group) {
     case 32:
-        return launch_g<T, MT, 32>(a, fused, spw, grid, waves, lds, s);
+        return launch_g<T, MT, 32>(a, fused, spw, grid, waves, ring, lds, s);
     case 64:
-        return launch_g<T, MT, 64>(a, fused, spw, grid, waves, lds, s);
+        return launch_g<T, MT, 64>(a, fused, spw, grid, waves, ring, lds, s);
     default:
-        return launch_g<T, MT, 128>(a, fused, spw, grid, waves, lds, s);
+        return launch_g<T, MT, 128>(a, fused, spw, grid, waves, ring, lds, s);
     }
 }
 
 template <class T>
-hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, size_t lds, hipStream_t s) {
-    return a.m <= 1 ? launch_m<T, 1>(a, group, fused, spw, grid, waves, lds, s) : launch_m<T, 16>(a, group, fused, spw, grid, waves, lds, s);
+hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
+    return a.m <= 1 ? launch_m<T, 1>(a, group, fused, spw, grid, waves, ring, lds, s)
+                    : launch_m<T, 16>(a, group, fused, spw, grid, waves, ring, lds, s);
 }
 
 } // namespace
@@ -705,8 +740,9 @@ hipError_t launch_args(const GemvArgs &a, const GemvCall &c, const GemvPlan &p, 
     }
     const dim3 grid(static_cast<unsigned>((p.groups + p.nu - 1) / p.nu), splits);
     const int group = static_cast<int>(c.w.group);
-    return c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream)
-                          : launch_dtype<BF16>(a, group, c.fused, p.spw, grid, p.waves, p.lds, stream);
+    const int ring = ring_depth(static_cast<int64_t>(grid.x) * grid.y * p.waves);
+    return c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, ring, p.lds, stream)
+                          : launch_dtype<BF16>(a, group, c.fused, p.spw, grid, p.waves, ring, p.lds, stream);
 }
 
 } // namespace
