@@ -288,9 +288,10 @@ def measured_traffic():
     return None
 
 
-def pmc_probe(hm, torch, dev, H, I, G, sets):
+def pmc_probe(hm, torch, dev, H, I, G, sets, rows=1):
     """Eager launches for one rocprofv3 --pmc pass: a copy kernel of known size (calibration), then the fused
-    gate_up GEMV and the down GEMV of the headline workload, on rotating weight sets."""
+    gate_up GEMV and the down GEMV of the headline workload (or of the same layer at `rows` rows), on rotating
+    weight sets."""
     words = (64 << 20) // 4
     bufs = [torch.empty(words, dtype=torch.int32, device=dev).random_(0, 1 << 30) for _ in range(4)]
     outs = [torch.empty_like(b) for b in bufs]
@@ -301,17 +302,17 @@ def pmc_probe(hm, torch, dev, H, I, G, sets):
     log(f"pmc probe: 8 copy launches of {words * 4} bytes read + {words * 4} bytes written")
     del bufs, outs
     layers = make_layers(hm, torch, dev, H, I, G, sets)
-    x = torch.randn((1, H), device=dev).to(torch.float16)
-    act = torch.empty((1, I), dtype=torch.float16, device=dev)
-    y = torch.empty((1, H), dtype=torch.float16, device=dev)
+    x = torch.randn((rows, H), device=dev).to(torch.float16)
+    act = torch.empty((rows, I), dtype=torch.float16, device=dev)
+    y = torch.empty((rows, H), dtype=torch.float16, device=dev)
     for r in range(2 * sets):
         layers[r % sets].gate_up(x, act)
     torch.cuda.synchronize()
-    log(f"pmc probe: {2 * sets} gate_up launches (M=1)")
+    log(f"pmc probe: {2 * sets} gate_up launches (M={rows})")
     for r in range(2 * sets):
         layers[r % sets].down(act, y)
     torch.cuda.synchronize()
-    log(f"pmc probe: {2 * sets} down launches (M=1)")
+    log(f"pmc probe: {2 * sets} down launches (M={rows})")
 
 
 def host_cpus():
@@ -405,6 +406,7 @@ def main():
     ap.add_argument("--sets", type=int, default=6, help="weight sets rotated per decode step")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the calibration copy and the headline GEMVs (for rocprofv3 --pmc passes)")
+    ap.add_argument("--rows", type=int, default=1, help="rows (M) of the --pmc-probe GEMVs")
     ap.add_argument("--pmc-probe-prefill", action="store_true",
                     help="only launch the fused gate_up GEMM at M=2048 (for rocprofv3 --pmc passes)")
     ap.add_argument("--profile", choices=("decode", "roofline"),
@@ -426,7 +428,7 @@ def main():
     out = {}
 
     if args.pmc_probe:
-        pmc_probe(hm, torch, dev, H, I, G, args.sets)
+        pmc_probe(hm, torch, dev, H, I, G, args.sets, args.rows)
         return
     if args.pmc_probe_prefill:
         pl = make_layers(hm, torch, dev, H, I, G, 2)
