@@ -194,18 +194,51 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
     }
     uint4 xv[kPre], wv[kPre] = {};
-    auto fetch = [&](int base) { // branch-free: chunks past the end re-read a valid one and are not staged
+    // Positions of this thread's next kPre chunks: row, chunk within the row, and whether it is staged (chunks
+    // past the end re-read a valid one, branch-free, and are not staged). One row: chunk idx of the wave's range.
+    // Several rows: a cursor that each chunk advances by the workgroup size (WGS chunks), so no chunk needs a
+    // division by the row length.
+    int prow[kPre], pc8[kPre];
+    bool pval[kPre];
+    int cur_row = 0, cur_c8 = 0;
+    if constexpr (MT > 1) {
+        cur_row = st_id / chunks_row;
+        cur_c8 = st_id - cur_row * chunks_row;
+    }
+    const int adv_q = MT > 1 ? WGS / chunks_row : 0;
+    const int adv_r = MT > 1 ? WGS - adv_q * chunks_row : 0;
+    auto positions = [&](int base) {
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            const int idx = st_hi > st_lo ? min(st_lo + base + c * st_step + st_id, st_hi - 1) : 0;
-            const int row = MT == 1 ? 0 : idx / chunks_row;
-            xv[c] = *reinterpret_cast<const uint4 *>(a.x + row * a.ldx + xk0 + (idx - row * chunks_row) * 8);
-            if (norm) {
-                wv[c] = *reinterpret_cast<const uint4 *>(a.norm_w + xk0 + idx * 8);
+            if constexpr (MT == 1) {
+                const int idx = st_lo + base + c * st_step + st_id;
+                pval[c] = idx < st_hi;
+                prow[c] = 0;
+                pc8[c] = st_hi > st_lo ? min(idx, st_hi - 1) : 0;
+            } else {
+                pval[c] = cur_row < m;
+                prow[c] = pval[c] ? cur_row : m - 1;
+                pc8[c] = pval[c] ? cur_c8 : chunks_row - 1;
+                cur_row += adv_q;
+                cur_c8 += adv_r;
+                if (cur_c8 >= chunks_row) {
+                    cur_c8 -= chunks_row;
+                    ++cur_row;
+                }
             }
         }
     };
-    fetch(0);
+    auto fetch = [&]() {
+#pragma unroll
+        for (int c = 0; c < kPre; ++c) {
+            xv[c] = *reinterpret_cast<const uint4 *>(a.x + prow[c] * a.ldx + xk0 + pc8[c] * 8);
+            if (norm) {
+                wv[c] = *reinterpret_cast<const uint4 *>(a.norm_w + xk0 + pc8[c] * 8);
+            }
+        }
+    };
+    positions(0);
+    fetch();
 
     // Scale/zero records travel in blocks of RB consecutive tiles: lane l loads the records of tile
     // i + l / 16 (column l % 16), so one coalesced load covers RB tiles (the records of consecutive tiles
@@ -298,9 +331,8 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 
     // 1. Stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes take
     //    consecutive 8-element chunks of a row, so one group is G / 8 consecutive lanes.
-    auto stage = [&](int idx, uint4 v, uint4 g, bool valid) {
+    auto stage = [&](int row, int c8, uint4 v, uint4 g, bool valid) {
         float sa = 0.0f, sb = 0.0f;
-        int row = 0, c8 = 0;
         if (norm) { // v <- round(v * scale * g) element-wise, as the RMSNorm kernel stores it
             uint32_t vw[4] = {v.x, v.y, v.z, v.w};
             const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
@@ -313,8 +345,6 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             v = uint4{vw[0], vw[1], vw[2], vw[3]};
         }
         if (valid) {
-            row = MT == 1 ? 0 : idx / chunks_row;
-            c8 = idx - row * chunks_row;
             if constexpr (T::kWide) {
                 // fp16: sums of the even / odd pairs with v_dot2_f32_f16 against (1, 1)
                 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -351,15 +381,14 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     };
 #pragma unroll
     for (int c = 0; c < kPre; ++c) {
-        const int idx = st_lo + c * st_step + st_id;
-        stage(idx, xv[c], wv[c], idx < st_hi); // all lanes take part in the shuffles
+        stage(prow[c], pc8[c], xv[c], wv[c], pval[c]); // all lanes take part in the shuffles
     }
     for (int base = kPre * st_step; st_lo + base < st_hi; base += kPre * st_step) {
-        fetch(base); // long ranges only: these chunks wait behind the first ring steps
+        positions(base);
+        fetch(); // long ranges only: these chunks wait behind the first ring steps
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            const int idx = st_lo + base + c * st_step + st_id;
-            stage(idx, xv[c], wv[c], idx < st_hi);
+            stage(prow[c], pc8[c], xv[c], wv[c], pval[c]);
         }
     }
     if constexpr (MT == 1) {
