@@ -107,8 +107,9 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// Dynamic LDS: xs [m][kc + 8] 16-bit, sums [m][kc / G + 1] float2 (Xb, X); after the multiply the front of
-// the same space holds red [waves][S][m][16] float.
+// Dynamic LDS: xs [m][kc + 8] 16-bit, sums [m][kc / G + 1] float2 (Xb, X), and red [waves][S][m][16] float:
+// at one row past the staging (and the RMSNorm's four partial sums), with several rows over its front after
+// the multiply.
 // RING: ring depth in steps for one row (MT == 1, group >= 64), at most 8 tiles; the other instantiations
 // size their ring themselves and take RING = 0.
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING>
@@ -147,8 +148,11 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int sst = kg + 1;
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
     float2 *sums = reinterpret_cast<float2 *>(smem + static_cast<size_t>(m) * xst * 2);
-    float *red = reinterpret_cast<float *>(smem);
     const int norm_off = (m * xst * 2 + m * sst * static_cast<int>(sizeof(float2)) + 15) & ~15; // 4 floats past the staging
+    // One row: the cross-wave sums get their own space past the norm's partials, so a wave that has finished its
+    // multiply writes them while others still read the staging (no barrier before the writes). Several rows:
+    // they reuse the staging space, which the 144 KiB chunk leaves no room beside.
+    float *red = reinterpret_cast<float *>(smem + (MT == 1 ? norm_off + 16 : 0));
 
     // This wave's strip group and its contiguous run [tb, te) of the split's tiles. Groups past the end of
     // the call (a partial last workgroup) read the last group and are not stored.
@@ -473,8 +477,10 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         step(u, tb + (rounds - 1) * KB + u);
     }
 
-    // 3. Add the waves of each strip group (red reuses the staging space), then write.
-    __syncthreads();
+    // 3. Add the waves of each strip group, then write.
+    if constexpr (MT > 1) {
+        __syncthreads(); // red reuses the staging space
+    }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
 #pragma unroll
@@ -721,8 +727,10 @@ GemvPlan plan_gemv(const GemvCall &c) {
     const int64_t kc = p.kt_per_split * 128;
     const size_t stage = static_cast<size_t>(c.m) * (kc + 8) * 2 + static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
     const size_t red = static_cast<size_t>(p.waves) * p.spw * c.m * 16 * sizeof(float);
-    // One row may also hold the RMSNorm's four partial sums past the staging area.
-    p.lds = std::max(((stage + 15) & ~static_cast<size_t>(15)) + (c.m == 1 ? 16 : 0), red);
+    // One row: the staging, the RMSNorm's four partial sums, then the cross-wave sums; several rows: the sums
+    // reuse the staging space.
+    const size_t stage16 = (stage + 15) & ~static_cast<size_t>(15);
+    p.lds = c.m == 1 ? stage16 + 16 + red : std::max(stage16, red);
     p.partial_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * c.m * strips * 16 * sizeof(float) : 0;
     return p;
 }
