@@ -121,6 +121,20 @@ template <class T> __device__ __forceinline__ uint4 magic_operand(uint32_t w, co
     return b;
 }
 
+// Buffer resource over [base, base + bytes): loads past the end return zero instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (buffer_load_dwordx4 ... lds); the
+// transfer counts in vmcnt until the bytes are in LDS. The host pass of hipcc does not instantiate kernels that
+// name this builtin, so only the device pass sees it.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
+#endif
+}
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations and is a compiler memory
 // barrier, but unlike __syncthreads() it does not wait for the wave's outstanding global loads (the
 // workgroup-scope fence of __syncthreads() waits for vmcnt(0)).

@@ -134,18 +134,6 @@ template <class T, int G, int NSW> struct BTile {
     uint32_t r[NSW][128 / G]; // scale/zero records of its groups
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
-
-// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (buffer_load_dwordx4 ... lds). The host
-// pass of hipcc does not instantiate kernels that name this builtin, so only the device pass sees it.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
-#endif
-}
-
 template <class T, int G, bool FUSED, int RBW, int NSW, int WN, int DEPTH>
 __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2))) gemm_kernel(GemmArgs a) {
     constexpr int WGS = WN * 64;

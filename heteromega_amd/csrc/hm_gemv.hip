@@ -22,14 +22,17 @@
 // with 4).
 //
 // Math per strip tile (4 MFMA steps of 32 K): the B operand is bias + q straight from the nibbles
-// (hm_device.hpp), A is the activation rows from LDS, so
+// (hm_device.hpp), A is the activation rows from LDS. One row:
 //   P = sum_k x'_k (bias + q'_k)       (q' = q, or 16 q on the fp16 odd pairs with x' = x / 16)
 //     = sum_k x_k q_k + Xb,            Xb = bias * sum_k x'_k
 // and per group, with scale s and zero z of the column, sum_k x_k (q_k - z) s = s (P - Xb - z X), X = sum_k x_k.
-// Xb and X per (row, group) are computed once when the workgroup stages x. This is the reference's
-// per-tile factorization s (sum q x - z sum x) (kernels/gpu/src/gemv_w4a16.cu:91-98,
-// src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:242-253), applied to MFMA partial sums. One LDS read of an
-// A fragment feeds the MFMAs of all S strips.
+// Xb and X per group are computed when the wave stages x. This is the reference's per-tile factorization
+// s (sum q x - z sum x) (kernels/gpu/src/gemv_w4a16.cu:91-98, src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:242-253),
+// applied to MFMA partial sums. Several rows: each 32-K step runs a second MFMA of the same A fragment against
+// the constant operand -(bias + z) (the fp16 odd pairs take bias 64, so x needs no scaling), so the chain holds
+// P = sum_k x_k (q_k - z) exactly in its products and the fold is one FMA s P per row: no per-group activation
+// sums, and x goes to LDS as it is, by DMA. The MFMA pipe has the room (it is idle most of the time in a
+// decode GEMV); the VALU has not. One LDS read of an A fragment feeds the MFMAs of all S strips.
 //
 // Output: plain y = round(sum) (or, accumulating, y = round(y + round(sum)): a residual add), fused
 // act = round(SiLU(gate) * up) with fp32 math and one rounding (kernels/gpu/src/silu_mul.cu:10-30), or fp32
@@ -107,9 +110,36 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// Dynamic LDS: xs [m][kc + 8] 16-bit, sums [m][kc / G + 1] float2 (Xb, X), and red [waves][S][m][16] float:
-// at one row past the staging (and the RMSNorm's four partial sums), with several rows over its front after
-// the multiply.
+// B operand of one 32-K step for several rows: bias + q in all eight K positions. fp16: 1024 + q in the even
+// pairs and 64 + q in the odd pairs, whose nibbles sit at bits 4..7 of each half (under the exponent of 64 the
+// mantissa step is 1/16, so 16 q reads as q); bf16: 128 + q (magic_operand).
+template <class T> __device__ __forceinline__ uint4 rows_operand(uint32_t w, const MagicRegs &c, uint32_t odd_magic) {
+    if constexpr (T::kWide) {
+        const uint32_t u = w >> 8;
+        return uint4{(w & c.lo) | c.magic, (w & c.hi) | odd_magic, (u & c.lo) | c.magic, (u & c.hi) | odd_magic};
+    } else {
+        return magic_operand<T>(w, c);
+    }
+}
+
+// The matching constant operand -(bias + z) for the zero point z of record r (bits 16..23, at most 16): every
+// value exact, so one MFMA of it against the same activations takes sum_k x_k (bias + z) off the step's sum.
+template <class T> __device__ __forceinline__ uint4 zero_operand(uint32_t r) {
+    const uint32_t z2 = __builtin_amdgcn_perm(0u, r, 0x0C020C02u); // z in both 16-bit halves
+    if constexpr (T::kWide) {
+        const uint32_t e = z2 | 0xE400E400u;        // -(1024 + z)
+        const uint32_t o = (z2 << 4) | 0xD400D400u; // -(64 + z)
+        return uint4{e, o, e, o};
+    } else {
+        const uint32_t e = z2 | 0xC300C300u; // -(128 + z)
+        return uint4{e, e, e, e};
+    }
+}
+
+// Dynamic LDS. One row: xs [kc + 8] 16-bit, sums [kc / G + 1] float2 (Xb, X), the RMSNorm's four partial sums,
+// then red [waves][S][16] float. Several rows: per K tile of the split a block of rows_pad = 4 ceil(m / 4) rows
+// of 256 bytes, the 16-byte chunk c of row r at slot c ^ (r % 16) (rows past m hold row m - 1), and after the
+// multiply red [waves][S][m][16] float over its front.
 // RING: ring depth in steps for one row (MT == 1, group >= 64), at most 8 tiles; the other instantiations
 // size their ring themselves and take RING = 0.
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING>
@@ -142,13 +172,15 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int kg = kc / G;    // groups of this split
     const int64_t xk0 = second ? static_cast<int64_t>(a.k0) : static_cast<int64_t>(kt0 - a.kt_begin) * 128;
 
-    // Row strides padded by 16 bytes (x) and 8 bytes (sums) so that lanes reading different rows of one MFMA
-    // operand or fold hit different LDS banks.
+    // One row: x padded by 16 bytes and the group sums by 8 (the layout the fold reads).
     const int xst = kc + 8;
     const int sst = kg + 1;
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
-    float2 *sums = reinterpret_cast<float2 *>(smem + static_cast<size_t>(m) * xst * 2);
-    const int norm_off = (m * xst * 2 + m * sst * static_cast<int>(sizeof(float2)) + 15) & ~15; // 4 floats past the staging
+    float2 *sums = reinterpret_cast<float2 *>(smem + xst * 2);
+    const int norm_off = (xst * 2 + sst * static_cast<int>(sizeof(float2)) + 15) & ~15; // 4 floats past the staging
+    // Several rows: bytes per K tile of the staged chunk.
+    const int rows_pad = (m + 3) & ~3;
+    const int tstride = rows_pad * 256;
     // One row: the cross-wave sums get their own space past the norm's partials, so a wave that has finished its
     // multiply writes them while others still read the staging (no barrier before the writes). Several rows:
     // they reuse the staging space, which the 144 KiB chunk leaves no room beside.
@@ -173,18 +205,15 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int te = min(tb + tpw, nkt);
     const int last = te - 1; // >= 0: a wave past the split's end gets te = nkt >= 1 and reads only zero-weighted tiles
 
-    // Activation staging. With one row each wave stages the K range of its own tiles, so no workgroup
-    // barrier stands between the weight stream and the multiply (waves of other strip groups with the same
-    // range write the same values). With several rows the workgroup stages the whole chunk once for its nu
-    // strip groups. Chunks are 8 consecutive K of one row; consecutive lanes take consecutive chunks, so one
-    // group's chunks are G / 8 consecutive lanes.
-    const int chunks_row = kc / 8;
-    const int st_lo = MT == 1 ? tb * 16 : 0;
-    const int st_hi = MT == 1 ? max(te, tb) * 16 : m * chunks_row;
-    const int st_step = MT == 1 ? 64 : WGS;
-    const int st_id = MT == 1 ? lane : tid;
-    // Memory requests go out in this order: the activation chunks this thread stages (held in registers),
-    // then the first KB steps of the wave's ring. Staging waits for the activations only.
+    // Activation staging. One row: each wave stages the K range of its own tiles, so no workgroup barrier
+    // stands between the weight stream and the multiply (waves of other strip groups with the same range write
+    // the same values). Chunks are 8 consecutive K; consecutive lanes take consecutive chunks, so one group's
+    // chunks are G / 8 consecutive lanes. Several rows: the workgroup copies the whole chunk once for its nu
+    // strip groups, memory to LDS without registers (below).
+    const int st_lo = tb * 16;
+    const int st_hi = max(te, tb) * 16;
+    // Memory requests go out in this order: the activation chunks (one row: held in registers; several rows:
+    // the LDS transfers), then the first KB steps of the wave's ring. Staging waits for the activations only.
     // RMSNorm of the row (one row, whole K): waves 0..3 take the norm's chunks of the 256 threads of the
     // separate RMSNorm kernel (thread t: elements 8t + 2048j), so its sum of squares is formed in the same order.
     const bool norm = MT == 1 && a.norm_w != nullptr;
@@ -198,51 +227,46 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
     }
     uint4 xv[kPre], wv[kPre] = {};
-    // Positions of this thread's next kPre chunks: row, chunk within the row, and whether it is staged (chunks
-    // past the end re-read a valid one, branch-free, and are not staged). One row: chunk idx of the wave's range.
-    // Several rows: a cursor that each chunk advances by the workgroup size (WGS chunks), so no chunk needs a
-    // division by the row length.
-    int prow[kPre], pc8[kPre];
+    // Positions of this thread's next kPre chunks of the wave's range and whether each is staged (chunks past the
+    // end re-read a valid one, branch-free, and are not staged).
+    int pc8[kPre];
     bool pval[kPre];
-    int cur_row = 0, cur_c8 = 0;
-    if constexpr (MT > 1) {
-        cur_row = st_id / chunks_row;
-        cur_c8 = st_id - cur_row * chunks_row;
-    }
-    const int adv_q = MT > 1 ? WGS / chunks_row : 0;
-    const int adv_r = MT > 1 ? WGS - adv_q * chunks_row : 0;
     auto positions = [&](int base) {
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            if constexpr (MT == 1) {
-                const int idx = st_lo + base + c * st_step + st_id;
-                pval[c] = idx < st_hi;
-                prow[c] = 0;
-                pc8[c] = st_hi > st_lo ? min(idx, st_hi - 1) : 0;
-            } else {
-                pval[c] = cur_row < m;
-                prow[c] = pval[c] ? cur_row : m - 1;
-                pc8[c] = pval[c] ? cur_c8 : chunks_row - 1;
-                cur_row += adv_q;
-                cur_c8 += adv_r;
-                if (cur_c8 >= chunks_row) {
-                    cur_c8 -= chunks_row;
-                    ++cur_row;
-                }
-            }
+            const int idx = st_lo + base + c * 64 + lane;
+            pval[c] = idx < st_hi;
+            pc8[c] = st_hi > st_lo ? min(idx, st_hi - 1) : 0;
         }
     };
     auto fetch = [&]() {
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            xv[c] = *reinterpret_cast<const uint4 *>(a.x + prow[c] * a.ldx + xk0 + pc8[c] * 8);
+            xv[c] = *reinterpret_cast<const uint4 *>(a.x + xk0 + pc8[c] * 8);
             if (norm) {
                 wv[c] = *reinterpret_cast<const uint4 *>(a.norm_w + xk0 + pc8[c] * 8);
             }
         }
     };
-    positions(0);
-    fetch();
+    if constexpr (MT == 1) {
+        positions(0);
+        fetch();
+    } else {
+        // Transfer p (1 KiB): K tile p / (rows_pad / 4), rows 4 (p % (rows_pad / 4)) + h; lane l fills slot l % 16
+        // of its row with chunk (l % 16) ^ row. Rows past m read row m - 1.
+        constexpr int WAVES = WGS / 64;
+        const int rblocks = rows_pad >> 2;
+        const uint32_t ldx2 = static_cast<uint32_t>(a.ldx) * 2u;
+        const __amdgpu_buffer_rsrc_t xr =
+            buffer_rsrc(a.x + xk0, static_cast<uint32_t>(m - 1) * ldx2 + static_cast<uint32_t>(kc) * 2u);
+        for (int p = wave; p < nkt * rblocks; p += WAVES) {
+            const int t = p / rblocks;
+            const int rb = p - t * rblocks;
+            const int row = 4 * rb + h;
+            const uint32_t voff = static_cast<uint32_t>(min(row, m - 1)) * ldx2 + static_cast<uint32_t>(col ^ row) * 16u;
+            lds_dma16(xr, smem + t * tstride + rb * 1024, voff, static_cast<uint32_t>(t) * 256u);
+        }
+    }
 
     // Scale/zero records travel in blocks of RB consecutive tiles: lane l loads the records of tile
     // i + l / 16 (column l % 16), so one coalesced load covers RB tiles (the records of consecutive tiles
@@ -298,6 +322,12 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     }
     __builtin_amdgcn_sched_barrier(0);
     advance();
+    if constexpr (MT > 1) {
+        // This wave's transfers are in LDS once at most the ring's loads are outstanding (vmcnt counts in issue
+        // order); the barrier then covers every wave's transfers.
+        wait_vmcnt<KB * S + (KB / RB) * S>();
+        lds_barrier();
+    }
 
     float nscale = 1.0f;
     if (norm) {
@@ -333,9 +363,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         nscale = 1.0f / sqrtf(total / static_cast<float>(hcols) + a.norm_eps);
     }
 
-    // 1. Stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes take
-    //    consecutive 8-element chunks of a row, so one group is G / 8 consecutive lanes.
-    auto stage = [&](int row, int c8, uint4 v, uint4 g, bool valid) {
+    // 1. One row: stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes
+    //    take consecutive 8-element chunks, so one group is G / 8 consecutive lanes.
+    auto stage = [&](int c8, uint4 v, uint4 g, bool valid) {
         float sa = 0.0f, sb = 0.0f;
         if (norm) { // v <- round(v * scale * g) element-wise, as the RMSNorm kernel stores it
             uint32_t vw[4] = {v.x, v.y, v.z, v.w};
@@ -373,53 +403,57 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
                 v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
                 v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
             }
-            *reinterpret_cast<uint4 *>(xs + row * xst + c8 * 8) = v;
+            *reinterpret_cast<uint4 *>(xs + c8 * 8) = v;
         }
         // Sum over the CPG consecutive lanes of a group with DPP (no LDS crossbar): pairs, quads, eights, sixteens.
         sa = group_sum<CPG>(sa);
         sb = group_sum<CPG>(sb);
         if (valid && (c8 % CPG) == 0) {
             const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
-            sums[row * sst + c8 / CPG] = make_float2(xb, sa + sb);
+            sums[c8 / CPG] = make_float2(xb, sa + sb);
         }
     };
-#pragma unroll
-    for (int c = 0; c < kPre; ++c) {
-        stage(prow[c], pc8[c], xv[c], wv[c], pval[c]); // all lanes take part in the shuffles
-    }
-    for (int base = kPre * st_step; st_lo + base < st_hi; base += kPre * st_step) {
-        positions(base);
-        fetch(); // long ranges only: these chunks wait behind the first ring steps
+    if constexpr (MT == 1) {
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            stage(prow[c], pc8[c], xv[c], wv[c], pval[c]);
+            stage(pc8[c], xv[c], wv[c], pval[c]); // all lanes take part in the shuffles
         }
-    }
-    if constexpr (MT == 1) {
+        for (int base = kPre * 64; st_lo + base < st_hi; base += kPre * 64) {
+            positions(base);
+            fetch(); // long ranges only: these chunks wait behind the first ring steps
+#pragma unroll
+            for (int c = 0; c < kPre; ++c) {
+                stage(pc8[c], xv[c], wv[c], pval[c]);
+            }
+        }
         // The wave reads only what it wrote; LDS operations of one wave complete in order.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    } else {
-        lds_barrier(); // not __syncthreads(): its fence would wait for the ring's loads too
     }
 
-    // 2. Multiply. A-operand row of this lane: rows >= m read row m - 1 instead; they only feed D rows >= m,
-    //    which are never stored.
-    const int arow = min(col, m - 1);
-    const uint16_t *xa = xs + arow * xst + 8 * h;
+    // 2. Multiply.
     const MagicRegs magic = magic_regs<T>();
-
     float acc[S][ROWS];
-    int srow[ROWS]; // staged rows of this lane's D elements
 #pragma unroll
     for (int e = 0; e < ROWS; ++e) {
-        srow[e] = min(4 * h + e, m - 1);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             acc[s][e] = 0.0f;
         }
     }
+    // One row: the lane's K offset in the staged row.
+    const uint16_t *xa = xs + 8 * h;
+    // Several rows: the A-operand row of this lane (rows past rows_pad read the last staged row; they only feed
+    // D rows >= m, which are never stored) and its slot offsets per 32-K step; the magic of the fp16 odd pairs.
+    const int arow = min(col, rows_pad - 1);
+    uint32_t aoff[4];
+#pragma unroll
+    for (int mu = 0; mu < 4; ++mu) {
+        aoff[mu] = static_cast<uint32_t>(arow * 256 + (((4 * mu + h) ^ arow) << 4));
+    }
+    uint32_t odd_magic = 0x54005400u;
+    asm volatile("" : "+v"(odd_magic));
 
-    // One step: the S tiles of local tile i (unclamped: tiles past the wave's run are weighted by zero).
+    // One row, one step: the S tiles of local tile i (unclamped: tiles past the wave's run are weighted by zero).
     auto step = [&](int u, int i) {
         const int ic = min(i, last);
         // Tiles past the wave's run are dropped by a select, not a zero weight: a wave without tiles reads
@@ -439,22 +473,55 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             }
             if (mu % SPG == SPG - 1) {
                 const int g = mu / SPG;
-                const int gl = ic * GPT + g; // local group index
-                float2 xsum[ROWS];
-#pragma unroll
-                for (int e = 0; e < ROWS; ++e) {
-                    xsum[e] = sums[srow[e] * sst + gl];
-                }
+                const float2 xsum = sums[ic * GPT + g];
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
                     const uint32_t rr = static_cast<uint32_t>(__shfl(static_cast<int>(rv[u / RB][s][g]), 16 * (u % RB) + col));
                     const float sc = T::to_float(rr & 0xFFFFu);
                     const float z = static_cast<float>((rr >> 16) & 0xFFu);
+                    const float t = __builtin_fmaf(-z, xsum.y, p[s][0] - xsum.x);
+                    const float upd = __builtin_fmaf(sc, t, acc[s][0]);
+                    acc[s][0] = live ? upd : acc[s][0];
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Several rows, one live step: the S tiles of local tile i. Each 32-K step chains the MFMA of bias + q and
+    // the MFMA of -(bias + z) into the group's sum P = sum_k x_k (q_k - z); the fold adds s P per row.
+    auto step_rows = [&](int u, int i) {
+        const uint8_t *at = smem + i * tstride;
+        float4_t p[S];
+        uint4 bz[S];
+        float sc[S];
+#pragma unroll
+        for (int mu = 0; mu < 4; ++mu) {
+            const uint4 av = *reinterpret_cast<const uint4 *>(at + aoff[mu]);
+            if (mu % SPG == 0) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const uint32_t rr = static_cast<uint32_t>(__shfl(static_cast<int>(rv[u / RB][s][mu / SPG]), 16 * (u % RB) + col));
+                    sc[s] = T::to_float(rr & 0xFFFFu);
+                    bz[s] = zero_operand<T>(rr);
+                    p[s] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const uint32_t word = mu == 0 ? wq[u][s].x : mu == 1 ? wq[u][s].y : mu == 2 ? wq[u][s].z : wq[u][s].w;
+                p[s] = T::mfma16(av, rows_operand<T>(word, magic, odd_magic), p[s]);
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                p[s] = T::mfma16(av, bz[s], p[s]);
+            }
+            if (mu % SPG == SPG - 1) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
 #pragma unroll
                     for (int e = 0; e < ROWS; ++e) {
-                        const float t = __builtin_fmaf(-z, xsum[e].y, p[s][e] - xsum[e].x);
-                        const float upd = __builtin_fmaf(sc, t, acc[s][e]);
-                        acc[s][e] = live ? upd : acc[s][e];
+                        acc[s][e] = __builtin_fmaf(sc[s], p[s][e], acc[s][e]);
                     }
                 }
             }
@@ -462,19 +529,31 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    const int rounds = (tpw + KB - 1) / KB; // the same for every wave of the workgroup
+    // One row: the same round count for every wave of the workgroup, the steps past a wave's run dropped by a
+    // select. Several rows: the wave's own count, so every step of a full round is live, and the last round
+    // skips its dead steps by a (wave-uniform) branch.
+    const int rounds = MT == 1 ? (tpw + KB - 1) / KB : max(1, (te - tb + KB - 1) / KB);
     for (int r = 0; r + 1 < rounds; ++r) {
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
             const int i = tb + r * KB + u;
-            step(u, i);
+            if constexpr (MT == 1) {
+                step(u, i);
+            } else {
+                step_rows(u, i);
+            }
             load(u, min(i + KB, last));
         }
         advance();
     }
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
-        step(u, tb + (rounds - 1) * KB + u);
+        const int i = tb + (rounds - 1) * KB + u;
+        if constexpr (MT == 1) {
+            step(u, i);
+        } else if (i < te) {
+            step_rows(u, i);
+        }
     }
 
     // 3. Add the waves of each strip group, then write.
@@ -663,9 +742,14 @@ GemvPlan plan_gemv(const GemvCall &c) {
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
     p.spw = c.fused ? 2 : (c.m > 1 && strips % 2 == 0 ? 2 : 1);
     p.groups = strips / p.spw;
+    // Staged activation bytes of a split of kts K tiles: one row, x and its group sums; several rows, rows_pad
+    // rows of x (m rounded up to a multiple of 4).
     auto stage_bytes = [&](int64_t kts) {
         const int64_t kc = kts * 128;
-        return static_cast<size_t>(c.m) * (kc + 8) * 2 + static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
+        if (c.m == 1) {
+            return static_cast<size_t>(kc + 8) * 2 + static_cast<size_t>(kc / c.w.group + 1) * sizeof(float2);
+        }
+        return static_cast<size_t>((c.m + 3) & ~int64_t{3}) * kc * 2;
     };
     auto set_splits = [&](int64_t splits) {
         splits = std::min<int64_t>(std::max<int64_t>(splits, 1), c.kt_count);
@@ -724,8 +808,7 @@ GemvPlan plan_gemv(const GemvCall &c) {
         }
     }
     p.waves = p.nu * p.wps;
-    const int64_t kc = p.kt_per_split * 128;
-    const size_t stage = static_cast<size_t>(c.m) * (kc + 8) * 2 + static_cast<size_t>(c.m) * (kc / c.w.group + 1) * sizeof(float2);
+    const size_t stage = stage_bytes(p.kt_per_split);
     const size_t red = static_cast<size_t>(p.waves) * p.spw * c.m * 16 * sizeof(float);
     // One row: the staging, the RMSNorm's four partial sums, then the cross-wave sums; several rows: the sums
     // reuse the staging space.
