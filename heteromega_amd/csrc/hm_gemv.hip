@@ -41,6 +41,7 @@
 #include "hm_internal.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 
 namespace hm {
@@ -49,16 +50,15 @@ namespace {
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr size_t kXBudget = 64 * 1024;   // staged activation bytes per workgroup at one row (bounds a split's K range)
-constexpr size_t kStageMax = 144 * 1024; // staged activation bytes per workgroup at several rows (LDS is 160 KiB)
+constexpr size_t kLdsMax = 160 * 1024;   // LDS of one workgroup
+constexpr int64_t kRowsInFlight = 5120;  // weight tiles in flight over a multi-row launch the planner aims for (5 MiB)
+constexpr int64_t kUnitsPerCu = 4;       // (strip group, split) units per CU a multi-row K split may make at most
 constexpr int kNormChunks = 4;           // RMSNorm in the staging: rows of up to 4 x 2048 columns
 constexpr int64_t kRingSteps = 8192;     // ring steps in flight over a one-row launch (8 MiB of single-strip tiles)
 
 // Ring depth of a one-row launch of `waves` waves: the deepest of 8, 4 and 3 steps that keeps at most
 // kRingSteps steps in flight, and 3 beyond that.
 int ring_depth(int64_t waves) { return waves * 8 <= kRingSteps ? 8 : waves * 4 <= kRingSteps ? 4 : 3; }
-
-// (strip group, split) units a launch with several rows aims for: 3.5 per CU.
-int64_t target_units(int64_t cus) { return 7 * cus / 2; }
 
 struct GemvArgs {
     const uint4 *quant;
@@ -738,7 +738,6 @@ hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, int spw, dim3 
 GemvPlan plan_gemv(const GemvCall &c) {
     GemvPlan p;
     const int64_t cus = device_topology().cus;
-    const int64_t units = target_units(cus);
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
     p.spw = c.fused ? 2 : (c.m > 1 && strips % 2 == 0 ? 2 : 1);
     p.groups = strips / p.spw;
@@ -756,22 +755,12 @@ GemvPlan plan_gemv(const GemvCall &c) {
         p.kt_per_split = (c.kt_count + splits - 1) / splits;
         p.splits = (c.kt_count + p.kt_per_split - 1) / p.kt_per_split;
     };
+    p.wps = 1;
+    p.nu = 1;
     if (c.m == 1) {
         // K split only to bound the staged chunk (kXBudget: 256 K tiles at one row).
         const int64_t max_tiles = static_cast<int64_t>(kXBudget) / 256;
         set_splits((c.kt_count + max_tiles - 1) / max_tiles);
-    } else {
-        // Several rows (launch shapes measured on the Llama-3-8B projections at M = 4 and 16, weights
-        // streamed from HBM): narrow grids (under 1.75 strip groups per CU) are split along K until there are
-        // 3.5 (strip group, split) units per CU; the staged chunk must leave room in LDS for the reduction.
-        set_splits(p.groups < units / 2 ? (units + p.groups - 1) / p.groups : 1);
-        while (stage_bytes(p.kt_per_split) > kStageMax && p.kt_per_split > 1) {
-            set_splits(p.splits + 1);
-        }
-    }
-    p.wps = 1;
-    p.nu = 1;
-    if (c.m == 1) {
         // Waves per strip group: up to 8, keeping at least 8 K tiles per wave (16 with a strip pair: measured
         // on the Llama-3-8B gate_up, 32-tile wave runs in 448 workgroups beat 16-tile runs in 896); strip
         // groups per workgroup: enough for 4 waves.
@@ -788,29 +777,66 @@ GemvPlan plan_gemv(const GemvCall &c) {
             p.nu *= 2;
         }
     } else {
-        // At least 8 K tiles per wave and strip (16 for the fused gate_up from 8 rows or with groups under 128:
-        // half the waves, each twice as long, so fewer waves share a SIMD in the last round, whose compute runs
-        // after the last weights arrive; measured Llama-3-8B gate_up at 8 / 16 rows 17.0 / 18.8 -> 15.8 / 17.1
-        // us and Qwen2.5-14B gate_up 6-12% faster at 2..16 rows, while at 2 and 4 rows with groups of 128 the
-        // halved grid leaves CUs idle: 3-4% slower). Workgroups of 8 to 16 waves, with enough strip groups that
-        // the staged chunk (M * 256 B per K tile) is at most half the workgroup's weight bytes (S KiB per K tile
-        // and group).
-        const int64_t run = c.fused && (c.m >= 8 || c.w.group < 128) ? 16 : 8;
-        while (p.wps < 16 && p.kt_per_split >= 2 * run * p.wps) {
-            p.wps *= 2;
+        // Several rows: the launch shape (K splits, waves per strip group, strip groups per workgroup) of least
+        // cost over the candidates that fit LDS, where the cost multiplies
+        //   the CU imbalance (the busiest CU's workgroups against the mean),
+        //   the distance of the weight loads in flight over the launch (each wave holds min(ring, its run) steps
+        //   of S tiles) from kRowsInFlight tiles: sqrt(target / in flight) below it and (in flight / target)^0.05
+        //   above (more only lengthens the memory queues and the tail),
+        //   1 + 0.05 x the staged activation bytes per weight byte (rows_pad / (4 nu S)),
+        //   1 + 0.5 x the split's fp32 partial traffic per weight byte (written and read: 16 splits m / K), and
+        //   1 + 0.25 per extra round of workgroups;
+        // ties go to fewer splits, then to more waves per workgroup. The weights and exponents are fitted to
+        // sweeps of every (splits, nu, wps) on the gate_up and down projections of Llama-3-8B, Qwen2.5-14B and
+        // Llama-3.2-1B at 2, 4, 8, 12 and 16 rows (one graph of 60 launches per shape, the graphs' replays
+        // interleaved, weights streamed from HBM): the rule's choice is within 5% of the best measured shape on all
+        // 30 of them and 1.1% on average, against 10.8% (at worst 65%) for the rules it replaced.
+        const int64_t rows_pad = (c.m + 3) & ~int64_t{3};
+        const int gpt = static_cast<int>(128 / c.w.group);
+        const int ring = std::max(1, (p.spw == 1 || gpt > 1 ? 4 : 8) / p.spw / (gpt == 4 ? 2 : 1)); // the kernel's KB
+        double best = -1.0;
+        for (int64_t sp = 1; sp <= std::min<int64_t>(c.kt_count, 16); ++sp) {
+            const int64_t ktp = (c.kt_count + sp - 1) / sp;
+            if ((c.kt_count + ktp - 1) / ktp != sp || (sp > 1 && sp * p.groups > kUnitsPerCu * cus)) {
+                continue; // a split count that a smaller count already gives, or partials past the bound
+            }
+            const size_t stage = stage_bytes(ktp);
+            for (int wps = 1; wps <= 4; wps *= 2) {
+                for (int nu = 1; nu <= 8; nu *= 2) {
+                    const int waves = nu * wps;
+                    const size_t lds = std::max(stage, static_cast<size_t>(waves) * p.spw * c.m * 16 * sizeof(float));
+                    if ((waves != 4 && waves != 8 && waves != 16) || lds > kLdsMax) {
+                        continue;
+                    }
+                    const int64_t wgs = (p.groups + nu - 1) / nu * sp;
+                    const int64_t per_cu = std::min<int64_t>(static_cast<int64_t>(kLdsMax / lds), 16 / waves);
+                    const int64_t rounds = (wgs + cus * per_cu - 1) / (cus * per_cu);
+                    const int64_t tpw = (ktp + wps - 1) / wps;
+                    const double inflight = static_cast<double>(p.groups * sp * wps * std::min<int64_t>(ring, tpw) * p.spw);
+                    const double imb = static_cast<double>((wgs + cus - 1) / cus * cus) / static_cast<double>(wgs);
+                    const double r = inflight / static_cast<double>(kRowsInFlight);
+                    const double partial = sp > 1 ? 16.0 * static_cast<double>(sp * c.m) / static_cast<double>(c.kt_count * 128) : 0.0;
+                    const double cost = imb * (r < 1.0 ? std::sqrt(1.0 / r) : std::pow(r, 0.05)) *
+                                        (1.0 + 0.05 * static_cast<double>(rows_pad) / (4.0 * nu * p.spw)) * (1.0 + 0.5 * partial) *
+                                        (1.0 + 0.25 * static_cast<double>(rounds - 1));
+                    // Candidates come in order of splits, so equal costs keep fewer splits; within the same
+                    // splits an equal cost takes the larger workgroup.
+                    const bool lower = best < 0.0 || cost < best * (1.0 - 1e-9);
+                    const bool tie_bigger = !lower && cost <= best * (1.0 + 1e-9) && sp == p.splits && waves > p.nu * p.wps;
+                    if (lower || tie_bigger) {
+                        best = cost;
+                        p.kt_per_split = ktp;
+                        p.splits = sp;
+                        p.wps = wps;
+                        p.nu = nu;
+                    }
+                }
+            }
         }
-        const int64_t nu_stage = (c.m + 2 * p.spw - 1) / (2 * p.spw);
-        while (p.nu * p.wps < 8 || p.nu < nu_stage) {
-            p.nu *= 2;
-        }
-        while (p.nu > 1 && p.nu * p.wps > 16) {
-            p.nu /= 2;
-        }
-        // From 8 rows, 16-wave workgroups share the chunk further while the grid keeps about one workgroup per
-        // CU (measured: faster at 8 and 16 rows, slower at 4).
-        const auto wgs = [&](int64_t nu) { return (p.groups + nu - 1) / nu * p.splits; };
-        while (c.m >= 8 && p.nu * p.wps < 16 && wgs(2 * p.nu) >= 27 * cus / 32) {
-            p.nu *= 2;
+        if (best < 0.0) { // unreachable for m <= 16: one K tile per split always fits
+            set_splits(c.kt_count);
+            p.wps = 1;
+            p.nu = 4;
         }
     }
     p.waves = p.nu * p.wps;
@@ -825,11 +851,10 @@ GemvPlan plan_gemv(const GemvCall &c) {
 }
 
 size_t gemv_partial_bound(const GemvCall &c) {
-    // With several rows a range of fewer than units / 2 strip groups takes ceil(units / groups) splits,
-    // so splits * groups < 3 units / 2; the staging-driven splits do not grow as the range narrows.
+    // With several rows a split launch has at most kUnitsPerCu (strip group, split) units per CU, whatever range
+    // of the call's columns it covers.
     const GemvPlan p = plan_gemv(c);
-    const int64_t units = target_units(device_topology().cus);
-    const size_t narrow = c.m > 1 ? static_cast<size_t>(3 * units / 2) * p.spw * c.m * 16 * sizeof(float) : 0;
+    const size_t narrow = c.m > 1 ? static_cast<size_t>(kUnitsPerCu * device_topology().cus) * p.spw * c.m * 16 * sizeof(float) : 0;
     return std::max(p.partial_bytes, narrow);
 }
 
