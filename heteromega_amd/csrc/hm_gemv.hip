@@ -139,7 +139,8 @@ template <class T> __device__ __forceinline__ uint4 zero_operand(uint32_t r) {
 // Dynamic LDS. One row: xs [kc + 8] 16-bit, sums [kc / G + 1] float2 (Xb, X), the RMSNorm's four partial sums,
 // then red [waves][S][16] float. Several rows: per K tile of the split a block of rows_pad = 4 ceil(m / 4) rows
 // of 256 bytes, the 16-byte chunk c of row r at slot c ^ (r % 16) (rows past m hold row m - 1), and after the
-// multiply red [waves][S][m][16] float over its front.
+// multiply, over its front, red [wps - 1][nu][S][4][64 lanes] float: the sums of each strip group's waves past
+// the first.
 // RING: ring depth in steps for one row (MT == 1, group >= 64), at most 8 tiles; the other instantiations
 // size their ring themselves and take RING = 0.
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING>
@@ -558,7 +559,63 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 
     // 3. Add the waves of each strip group, then write.
     if constexpr (MT > 1) {
-        __syncthreads(); // red reuses the staging space
+        // Several rows: the group's first wave (K range 0) writes the outputs straight from its accumulators
+        // (lane: column col, rows 4 h + e), after adding those of the group's other waves in order of their K
+        // ranges, which they leave in LDS lane by lane; a group of one wave needs neither LDS nor a barrier.
+        // The sums are the same as adding every wave's share to zero in that order (no share is -0).
+        const int gg = static_cast<int>(blockIdx.x) * a.nu + grp;
+        if (a.wps > 1) {
+            __syncthreads(); // red reuses the staging space
+            if (wi > 0) {
+                float *rw = red + ((wi - 1) * a.nu + grp) * (S * ROWS * 64) + lane;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+#pragma unroll
+                    for (int e = 0; e < ROWS; ++e) {
+                        rw[(s * ROWS + e) * 64] = acc[s][e];
+                    }
+                }
+            }
+            __syncthreads();
+            if (wi == 0) {
+                for (int w = 1; w < a.wps; ++w) {
+                    const float *rr = red + ((w - 1) * a.nu + grp) * (S * ROWS * 64) + lane;
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+#pragma unroll
+                        for (int e = 0; e < ROWS; ++e) {
+                            acc[s][e] += rr[(s * ROWS + e) * 64];
+                        }
+                    }
+                }
+            }
+        }
+        if (wi == 0 && gg < a.groups) {
+#pragma unroll
+            for (int e = 0; e < ROWS; ++e) {
+                const int row = 4 * h + e;
+                if (row >= m) {
+                    continue;
+                }
+                if (a.partial != nullptr) {
+                    float *pr = a.partial + (static_cast<int64_t>(split) * m + row) * a.ncols + gg * S * 16 + col;
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        pr[s * 16] = acc[s][e];
+                    }
+                } else if constexpr (FUSED) {
+                    a.y[row * a.ldy + gg * 16 + col] = T::from_float(silu(acc[0][e]) * acc[1][e]);
+                } else {
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        uint16_t *yp = a.y + row * a.ldy + (gg * S + s) * 16 + col;
+                        const uint16_t yv = T::from_float(acc[s][e]);
+                        *yp = a.accumulate ? T::from_float(T::to_float(*yp) + T::to_float(yv)) : yv;
+                    }
+                }
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -750,6 +807,9 @@ GemvPlan plan_gemv(const GemvCall &c) {
         }
         return static_cast<size_t>((c.m + 3) & ~int64_t{3}) * kc * 2;
     };
+    // Several rows: LDS for the cross-wave sums, a lane-contiguous block of S x 4 rows for each wave past the
+    // first of a strip group (over the staging space, after the multiply).
+    auto rows_red = [&](int64_t wps, int64_t nu) { return static_cast<size_t>((wps - 1) * nu * p.spw * 4 * 64) * sizeof(float); };
     auto set_splits = [&](int64_t splits) {
         splits = std::min<int64_t>(std::max<int64_t>(splits, 1), c.kt_count);
         p.kt_per_split = (c.kt_count + splits - 1) / splits;
@@ -804,7 +864,7 @@ GemvPlan plan_gemv(const GemvCall &c) {
             for (int wps = 1; wps <= 4; wps *= 2) {
                 for (int nu = 1; nu <= 8; nu *= 2) {
                     const int waves = nu * wps;
-                    const size_t lds = std::max(stage, static_cast<size_t>(waves) * p.spw * c.m * 16 * sizeof(float));
+                    const size_t lds = std::max(stage, rows_red(wps, nu));
                     if ((waves != 4 && waves != 8 && waves != 16) || lds > kLdsMax) {
                         continue;
                     }
@@ -841,7 +901,7 @@ GemvPlan plan_gemv(const GemvCall &c) {
     }
     p.waves = p.nu * p.wps;
     const size_t stage = stage_bytes(p.kt_per_split);
-    const size_t red = static_cast<size_t>(p.waves) * p.spw * c.m * 16 * sizeof(float);
+    const size_t red = c.m == 1 ? static_cast<size_t>(p.waves) * p.spw * 16 * sizeof(float) : rows_red(p.wps, p.nu);
     // One row: the staging, the RMSNorm's four partial sums, then the cross-wave sums; several rows: the sums
     // reuse the staging space.
     const size_t stage16 = (stage + 15) & ~static_cast<size_t>(15);
