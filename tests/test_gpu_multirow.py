@@ -1,0 +1,66 @@
+"""GPU: decode GEMVs at several rows against the float64 oracle, through the C ABI, on shapes chosen to reach
+the multi-row launch-shape rule's corners: narrow outputs split along K (up to 16 splits, several waves per strip
+group reducing through LDS), wide outputs with one wave per strip group, odd row counts (rows padded to a
+multiple of 4 in the staged chunk), the fused SwiGLU, and zero points up to 16 (the largest a GPTQ checkpoint
+gives after adding its one back), which the multi-row kernel takes off with the exact operand -(bias + z)."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TORCH, assert_close, host_f64, logical_to_device, make_x
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("m", [1, 3, 16, 40])
+def test_zero_point_sixteen(oracle, hm, device, dtype, m):
+    rng = np.random.default_rng(700 + m)
+    k, n, g = 1024, 512, 128
+    w_np = oracle.random_weights(rng, k, n, g, dtype, z_lo=12, z_hi=17)
+    assert w_np[2].max() == 16
+    w = hm.RepackedMatrix.from_logical(*logical_to_device(w_np, dtype, device), g, dtype=TORCH[dtype])
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=TORCH[dtype], device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, g, dtype), dtype, f"zero 16 M={m}")
+
+
+@pytest.mark.parametrize("m", [2, 6, 11, 16])
+@pytest.mark.parametrize("k,n,g,dtype", [
+    (8192, 256, 128, "fp16"),   # 8 strip pairs: many K splits, several waves per group
+    (4096, 1024, 64, "bf16"),   # narrow, groups of 64 (shallower ring)
+    (1024, 8192, 128, "fp16"),  # wide: one wave per strip group, no split
+    (2048, 2048, 32, "fp16"),   # groups of 32
+])
+def test_multirow_launch_shapes(oracle, hm, device, m, k, n, g, dtype):
+    rng = np.random.default_rng(800 + m + k // 128 + n // 16 + g)
+    w_np = oracle.random_weights(rng, k, n, g, dtype)
+    w = hm.RepackedMatrix.from_logical(*logical_to_device(w_np, dtype, device), g, dtype=TORCH[dtype])
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=TORCH[dtype], device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, g, dtype), dtype, f"linear M={m} [{k}x{n}] g={g} {dtype}")
+
+
+@pytest.mark.parametrize("m", [3, 8, 13])
+def test_multirow_fused_gate_up(oracle, hm, device, m):
+    # A small FFN's gate_up at several rows: SwiGLU of the two strips of each pair, written from the first wave of
+    # the strip group (or by sum_splits where the rule splits K), against the oracle's single-rounding SwiGLU.
+    rng = np.random.default_rng(900 + m)
+    hidden, inter, g, dtype = 2048, 3072, 128, "fp16"
+    gate_np = oracle.random_weights(rng, hidden, inter, g, dtype)
+    up_np = oracle.random_weights(rng, hidden, inter, g, dtype)
+    down_np = oracle.random_weights(rng, inter, hidden, g, dtype)
+    ffn = hm.FfnLayer.from_logical(*(logical_to_device(w, dtype, device) for w in (gate_np, up_np, down_np)), g, dtype=TORCH[dtype])
+    x64, x = make_x(oracle, rng, m, hidden, dtype, device)
+    act = torch.empty((m, inter), dtype=TORCH[dtype], device=device)
+    ffn.gate_up(x, act)
+    torch.cuda.synchronize()
+    gate = x64 @ oracle.weights_f64(*gate_np, g, dtype)
+    up = x64 @ oracle.weights_f64(*up_np, g, dtype)
+    ref = oracle.silu(gate) * up
+    assert_close(oracle, host_f64(act), ref, dtype, f"gate_up M={m}")
