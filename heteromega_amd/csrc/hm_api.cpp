@@ -373,6 +373,8 @@ hm_status build_ffn_from_tiles(const hm::TileSource gu[2], const uint8_t *down, 
     });
 }
 
+size_t one_row_spill_bytes(int64_t channels) { return static_cast<size_t>(round_up(static_cast<int64_t>(hm::gemv_pair_spill_bytes(channels)), 256)); }
+
 } // namespace
 
 hm::Topology hm::device_topology() {
@@ -943,7 +945,8 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
     if (f == nullptr || max_m <= 0) {
         return 0;
     }
-    const size_t act = static_cast<size_t>(round_up(max_m * f->inter * 2, 256));
+    // The one-row layout (act, the strip-pair spill, partials) fits in the same bytes as every wider one.
+    const size_t act = static_cast<size_t>(round_up(max_m * f->inter * 2, 256)) + one_row_spill_bytes(f->inter);
     // The largest partial buffer of any M up to max_m and any channel range: the GEMV's (M <= 16, planned when the
     // layer was made) and, above, the GEMM's small-grid K split, which never needs more than kGemmPartialMax.
     if (max_m <= kGemvMaxRows) {
@@ -951,6 +954,81 @@ size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m) {
     }
     return act + std::max(hm::kGemmPartialMax, f->decode_partial[kGemvMaxRows]);
 }
+
+namespace {
+
+// One row through the two GEMVs: act = SwiGLU(x W_gate_up) over channels [ch_begin, ch_end) (of RMSNorm(x) *
+// norm_w when norm_w is given; hidden <= 8192), then y = act W_down (accumulate: y += it, rounded). Workspace:
+// act, the strip-pair spill, then split partials. With the spill the gate_up GEMV may deal its strip pairs' K
+// halves evenly over the CUs; the down GEMV then forms the act columns of the pairs two workgroups share.
+hm_status one_row_ffn(const hm_ffn *f, void *y, int64_t ldy, const void *x, int64_t ldx, int64_t ch_begin, int64_t ch_end,
+                      const void *norm_w, float eps, bool accumulate, void *workspace, size_t workspace_bytes, hipStream_t s) {
+    const int64_t n = ch_end - ch_begin;
+    const size_t act_bytes = static_cast<size_t>(round_up(n * 2, 256));
+    const size_t spill_bytes = one_row_spill_bytes(n);
+    if (workspace_bytes < act_bytes + spill_bytes) {
+        return fail(HM_WORKSPACE_TOO_SMALL, "one-row FFN: workspace of %zu bytes, need %zu before partials", workspace_bytes,
+                    act_bytes + spill_bytes);
+    }
+    uint16_t *act = static_cast<uint16_t *>(workspace);
+    float *spill = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + act_bytes);
+    void *rest = static_cast<uint8_t *>(workspace) + act_bytes + spill_bytes;
+    const size_t rest_bytes = workspace_bytes - act_bytes - spill_bytes;
+    hm::GemvCall c;
+    c.w = f->gate_up.p;
+    c.x = static_cast<const uint16_t *>(x);
+    c.ldx = ldx;
+    c.y = act;
+    c.ldy = n;
+    c.m = 1;
+    c.strip_begin = 2 * (ch_begin / 16);
+    c.n = n;
+    c.kt_count = f->hidden / 128;
+    c.fused = true;
+    c.norm_w = static_cast<const uint16_t *>(norm_w);
+    c.norm_eps = eps;
+    c.pair_spill = spill;
+    c.partial = static_cast<float *>(rest);
+    hm::GemvPlan gp = hm::plan_gemv(c);
+    hm::GemvCall d;
+    d.w = f->down.p;
+    d.x = act;
+    d.ldx = n;
+    d.y = static_cast<uint16_t *>(y);
+    d.ldy = ldy;
+    d.m = 1;
+    d.n = f->hidden;
+    d.kt_begin = ch_begin / 128;
+    d.kt_count = n / 128;
+    d.accumulate = accumulate;
+    d.partial = c.partial;
+    if (gp.units % 2 == 1) {
+        d.pair_spill = spill;
+        d.pair_units = gp.units;
+        // The down GEMV forms the split pairs in every strip group of a workgroup; with more than one, or more LDS
+        // than a workgroup has, the gate_up keeps whole pairs per workgroup (Qwen2.5-14B, two down strip groups
+        // per workgroup: 26.9 us a layer against 26.0).
+        const hm::GemvPlan dp = hm::plan_gemv(d);
+        if (dp.nu > 1 || dp.lds > hm::kGemvLdsMax) {
+            c.pair_spill = nullptr;
+            gp = hm::plan_gemv(c);
+            d.pair_spill = nullptr;
+            d.pair_units = 0;
+        }
+    }
+    const size_t need = std::max(gp.partial_bytes, hm::plan_gemv(d).partial_bytes);
+    if (need > rest_bytes) {
+        return fail(HM_WORKSPACE_TOO_SMALL, "one-row FFN: %zu bytes for partials, need %zu", rest_bytes, need);
+    }
+    hipError_t e = hm::launch_gemv(c, s);
+    if (e != hipSuccess) {
+        return hip_fail(e, "one-row gate_up launch");
+    }
+    e = hm::launch_gemv(d, s);
+    return e == hipSuccess ? HM_OK : hip_fail(e, "one-row down launch");
+}
+
+} // namespace
 
 hm_status hm_ffn_gate_up(const hm_ffn *f, void *act, int64_t ld_act, const void *x, int64_t ldx, int64_t M, int64_t ch_begin, int64_t ch_end,
                          void *workspace, size_t workspace_bytes, void *stream) {
@@ -993,6 +1071,13 @@ hm_status hm_ffn_forward(const hm_ffn *f, void *y, int64_t ldy, const void *x, i
     if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)) {
         return fail(HM_WORKSPACE_TOO_SMALL, "hm_ffn_forward: workspace must be 256-byte aligned with >= %zu bytes (got %zu)", need,
                     workspace_bytes);
+    }
+    if (M == 1) {
+        if ((st = check_activation(x, ldx, f->hidden, "hm_ffn_forward x")) != HM_OK ||
+            (st = check_output(y, ldy, f->hidden, "hm_ffn_forward y")) != HM_OK) {
+            return st;
+        }
+        return one_row_ffn(f, y, ldy, x, ldx, ch_begin, ch_end, nullptr, 0.0f, false, workspace, workspace_bytes, as_stream(stream));
     }
     const int64_t n = ch_end - ch_begin;
     const size_t act_bytes = static_cast<size_t>(round_up(M * f->inter * 2, 256));
@@ -1039,38 +1124,7 @@ hm_status hm_ffn_block_forward(const hm_ffn *f, void *x, int64_t ldx, const void
     const hm_dtype dtype = static_cast<hm_dtype>(f->gate_up.p.dtype);
     if (M == 1 && f->hidden <= 8192) {
         // Two launches: the gate_up GEMV stages RMSNorm(x) * weight, the down GEMV adds its output into x.
-        uint16_t *act = static_cast<uint16_t *>(ffn_ws);
-        const size_t act_bytes = static_cast<size_t>(round_up(f->inter * 2, 256));
-        hm::GemvCall c;
-        c.w = f->gate_up.p;
-        c.x = static_cast<const uint16_t *>(x);
-        c.ldx = ldx;
-        c.y = act;
-        c.ldy = f->inter;
-        c.m = 1;
-        c.n = f->inter;
-        c.kt_count = f->hidden / 128;
-        c.fused = true;
-        c.norm_w = static_cast<const uint16_t *>(norm_weight);
-        c.norm_eps = eps;
-        c.partial = reinterpret_cast<float *>(static_cast<uint8_t *>(ffn_ws) + act_bytes);
-        hipError_t e = hm::launch_gemv(c, s);
-        if (e != hipSuccess) {
-            return hip_fail(e, "block gate_up launch");
-        }
-        hm::GemvCall d;
-        d.w = f->down.p;
-        d.x = act;
-        d.ldx = f->inter;
-        d.y = static_cast<uint16_t *>(x);
-        d.ldy = ldx;
-        d.m = 1;
-        d.n = f->hidden;
-        d.kt_count = f->inter / 128;
-        d.accumulate = true;
-        d.partial = c.partial;
-        e = hm::launch_gemv(d, s);
-        return e == hipSuccess ? HM_OK : hip_fail(e, "block down launch");
+        return one_row_ffn(f, x, ldx, x, ldx, 0, f->inter, norm_weight, eps, true, ffn_ws, ffn_bytes, s);
     }
     // Several rows: RMSNorm, the FFN, the residual add (the same results as the two-launch path per row).
     if ((st = hm_rmsnorm(normed, f->hidden, x, ldx, norm_weight, M, f->hidden, eps, dtype, stream)) != HM_OK ||

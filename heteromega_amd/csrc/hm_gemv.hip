@@ -50,7 +50,7 @@ namespace {
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr size_t kXBudget = 64 * 1024;   // staged activation bytes per workgroup at one row (bounds a split's K range)
-constexpr size_t kLdsMax = 160 * 1024;   // LDS of one workgroup
+constexpr size_t kLdsMax = kGemvLdsMax;   // LDS of one workgroup
 constexpr int64_t kRowsInFlight = 5120;  // weight tiles in flight over a multi-row launch the planner aims for (5 MiB)
 constexpr int64_t kUnitsPerCu = 4;       // (strip group, split) units per CU a multi-row K split may make at most
 constexpr int kNormChunks = 4;           // RMSNorm in the staging: rows of up to 4 x 2048 columns
@@ -84,6 +84,14 @@ struct GemvArgs {
     const uint32_t *meta2;
     int kt_pitch2, kt_count2;
     int k0;
+    // One row, fused: units > 0 deals (strip pair, K half) units evenly over the workgroups, workgroup b running
+    // units b * units .. b * units + units - 1 (unit u: pair u / 2, half u % 2); a pair whose two units fall in
+    // two workgroups (odd units) writes both halves' fp32 sums to pair_spill instead of its act columns.
+    int units;
+    // One row, plain: pair_units > 0 (odd) means x is the act of such a launch with that many units per
+    // workgroup, whose split pairs' columns are formed from pair_spill while x is staged.
+    int pair_units;
+    float *pair_spill;
 };
 
 // v plus v of another lane of the same row of 16 (DPP control CTRL).
@@ -137,14 +145,17 @@ template <class T> __device__ __forceinline__ uint4 zero_operand(uint32_t r) {
 }
 
 // Dynamic LDS. One row: xs [kc + 8] 16-bit, sums [kc / G + 1] float2 (Xb, X), the RMSNorm's four partial sums,
-// then red [waves][S][16] float. Several rows: per K tile of the split a block of rows_pad = 4 ceil(m / 4) rows
-// of 256 bytes, the 16-byte chunk c of row r at slot c ^ (r % 16) (rows past m hold row m - 1), and after the
-// multiply, over its front, red [wps - 1][nu][S][4][64 lanes] float: the sums of each strip group's waves past
-// the first.
+// red [waves][S][16] float, then (pair_units > 0) the formed columns of the split's split pairs, 16 per pair in
+// pair order. Several rows: per K tile of the split a block of rows_pad = 4 ceil(m / 4) rows of 256 bytes, the
+// 16-byte chunk c of row r at slot c ^ (r % 16) (rows past m hold row m - 1), and after the multiply, over its
+// front, red [wps - 1][nu][S][4][64 lanes] float: the sums of each strip group's waves past the first.
 // RING: ring depth in steps for one row (MT == 1, group >= 64), at most 8 tiles; the other instantiations
-// size their ring themselves and take RING = 0.
-template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING>
+// size their ring themselves and take RING = 0. PAIRS (one row): kUnitsOut, the fused launch by units (a.units
+// waves per workgroup of WGS = 1024); kUnitsIn, the plain launch whose x holds such a launch's split pairs.
+constexpr int kUnitsOut = 1, kUnitsIn = 2;
+template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING, int PAIRS = 0>
 __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) gemv_kernel(GemvArgs a) {
+    static_assert(PAIRS == 0 || (MT == 1 && (PAIRS == kUnitsOut ? FUSED && WGS == 1024 : !FUSED && S == 1)), "pair modes");
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int ROWS = MT == 1 ? 1 : 4; // D elements per lane that can hold a real row
     constexpr int GPT = 128 / G;           // groups per strip tile
@@ -188,10 +199,13 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     float *red = reinterpret_cast<float *>(smem + (MT == 1 ? norm_off + 16 : 0));
 
     // This wave's strip group and its contiguous run [tb, te) of the split's tiles. Groups past the end of
-    // the call (a partial last workgroup) read the last group and are not stored.
-    const int grp = wave % a.nu;
-    const int wi = wave / a.nu;
-    const int gidx = min(static_cast<int>(blockIdx.x) * a.nu + grp, a.groups - 1);
+    // the call (a partial last workgroup) read the last group and are not stored. Units (one row, fused): the
+    // wave's unit gives its pair and its K half (a.wps == 2).
+    constexpr bool by_units = PAIRS == kUnitsOut;
+    const int unit = static_cast<int>(blockIdx.x) * a.units + wave;
+    const int grp = by_units ? 0 : wave % a.nu;
+    const int wi = by_units ? unit & 1 : wave / a.nu;
+    const int gidx = min(by_units ? unit >> 1 : static_cast<int>(blockIdx.x) * a.nu + grp, a.groups - 1);
     const int strip0 = a.strip_begin + gidx * S;
     const uint4 *qp[S];
     const uint32_t *mp[S];
@@ -249,9 +263,34 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             }
         }
     };
+    // Split pairs of the producing launch (one row, plain, pair_units = U odd): pair p of x's columns is split
+    // when p % U == (U - 1) / 2, and split pair U j + (U - 1) / 2 has the fp32 sums of its column c at pair_spill
+    // [16 j + c] = {gate, up of half 0, gate, up of half 1}. The wave's split pairs' columns t (16 per pair) are
+    // taken four per lane, t = lane + 64 i, their sums loaded ahead of the weights; before staging each is formed
+    // as round(SiLU(g0 + g1) * (u0 + u1)), the rounding of the producer's other pairs, into the LDS area `formed`
+    // (the split's split pairs in order, 16 columns each), which the staging reads in place of x.
+    constexpr bool forms = PAIRS == kUnitsIn;
+    constexpr int kFormPre = 4; // columns per lane loaded ahead (a range with more forms the rest after)
+    const int pu = forms ? a.pair_units : 1;
+    const int phalf = (pu - 1) >> 1;
+    const int cb = static_cast<int>(xk0 >> 3);                       // x chunk of the split's first K
+    const int js = (cb / 2 + phalf) / pu;                             // the split's first split pair
+    const int ja = uniform(((cb + st_lo) / 2 + phalf) / pu);          // this wave's first split pair
+    const int ncols_form = forms ? 16 * (uniform(((cb + st_hi) / 2 + phalf) / pu) - ja) : 0;
+    uint16_t *formed = reinterpret_cast<uint16_t *>(smem + norm_off + 16 + (WGS / 64) * S * 16 * static_cast<int>(sizeof(float)));
+    const float4 *spill4 = reinterpret_cast<const float4 *>(a.pair_spill) + static_cast<int64_t>(ja) * 16;
+    float4 fsum[kFormPre];
     if constexpr (MT == 1) {
         positions(0);
         fetch();
+        if constexpr (forms) {
+            if (ncols_form > 0) { // columns past the range re-read its last one
+#pragma unroll
+                for (int i = 0; i < kFormPre; ++i) {
+                    fsum[i] = spill4[min(lane + 64 * i, ncols_form - 1)];
+                }
+            }
+        }
     } else {
         // Transfer p (1 KiB): K tile p / (rows_pad / 4), rows 4 (p % (rows_pad / 4)) + h; lane l fills slot l % 16
         // of its row with chunk (l % 16) ^ row. Rows past m read row m - 1.
@@ -414,17 +453,46 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             sums[c8 / CPG] = make_float2(xb, sa + sb);
         }
     };
+    // x's chunk c8 of the split, or its formed chunk when it belongs to a split pair. pr / pu as the high word of
+    // pr ceil(2^32 / pu): exact for pr < 2^28 (pu <= 16).
+    const uint32_t pu_inv = forms ? 0xFFFFFFFFu / static_cast<uint32_t>(pu) + 1u : 0u;
+    auto x_chunk = [&](int c8, uint4 v) {
+        if constexpr (forms) {
+            const int k8 = cb + c8;
+            const int pr = k8 >> 1;
+            const int q = static_cast<int>(__umulhi(static_cast<uint32_t>(pr), pu_inv));
+            if (pr - q * pu == phalf) {
+                v = reinterpret_cast<const uint4 *>(formed)[(q - js) * 2 + (k8 & 1)];
+            }
+        }
+        return v;
+    };
     if constexpr (MT == 1) {
+        if constexpr (forms) {
+            uint16_t *fw = formed + (ja - js) * 16;
+            auto form = [&](int t, float4 v) {
+                if (t < ncols_form) {
+                    fw[t] = T::from_float(silu((0.0f + v.x) + v.z) * ((0.0f + v.y) + v.w));
+                }
+            };
+#pragma unroll
+            for (int i = 0; i < kFormPre; ++i) {
+                form(lane + 64 * i, fsum[i]);
+            }
+            for (int t = lane + 64 * kFormPre; t < ncols_form; t += 64) {
+                form(t, spill4[t]);
+            }
+        }
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            stage(pc8[c], xv[c], wv[c], pval[c]); // all lanes take part in the shuffles
+            stage(pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]); // all lanes take part in the shuffles
         }
         for (int base = kPre * 64; st_lo + base < st_hi; base += kPre * 64) {
             positions(base);
             fetch(); // long ranges only: these chunks wait behind the first ring steps
 #pragma unroll
             for (int c = 0; c < kPre; ++c) {
-                stage(pc8[c], xv[c], wv[c], pval[c]);
+                stage(pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]);
             }
         }
         // The wave reads only what it wrote; LDS operations of one wave complete in order.
@@ -617,6 +685,35 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
         return;
     }
+    if constexpr (by_units) {
+        {
+            // The halves' sums meet in red [wave][S][16]. A pair whose partner wave is in this workgroup is
+            // finished by its first half; a split pair (the last wave's first half, the first wave's second half)
+            // leaves both halves' sums in the spill.
+            if (h == 0) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    red[(wave * S + s) * 16 + col] = acc[s][0];
+                }
+            }
+            __syncthreads();
+            const int pair = unit >> 1;
+            if (h == 0 && pair < a.groups) {
+                if (wi == 0 ? wave + 1 == a.units : wave == 0) {
+                    float *sp = a.pair_spill + (static_cast<int64_t>(pair / a.units) * 16 + col) * 4 + wi * 2;
+                    *reinterpret_cast<float2 *>(sp) = make_float2(acc[0][0], acc[1][0]);
+                } else if (wi == 0) {
+                    float v[S];
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        v[s] = (0.0f + red[(wave * S + s) * 16 + col]) + red[((wave + 1) * S + s) * 16 + col];
+                    }
+                    a.y[gidx * 16 + col] = T::from_float(silu(v[0]) * v[1]);
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
 #pragma unroll
@@ -716,9 +813,9 @@ __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ part
     y[row * ldy + c] = accumulate ? T::from_float(T::to_float(y[row * ldy + c]) + T::to_float(out)) : out;
 }
 
-template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING>
-hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
-    auto kern = gemv_kernel<T, MT, G, S, FUSED, WGS, RING>;
+template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING, int PAIRS>
+hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s, unsigned block) {
+    auto kern = gemv_kernel<T, MT, G, S, FUSED, WGS, RING, PAIRS>;
     // One attribute call per instantiation; a function-local static is initialized once even when several
     // host threads launch at the same time.
     static const hipError_t configured =
@@ -726,31 +823,52 @@ hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s) {
     if (configured != hipSuccess) {
         return configured;
     }
-    hipLaunchKernelGGL(kern, grid, dim3(WGS), lds, s, a);
+    hipLaunchKernelGGL(kern, grid, dim3(block), lds, s, a);
     return hipGetLastError();
 }
 
-template <class T, int MT, int G, int S, bool FUSED, int WGS>
-hipError_t launch_r(const GemvArgs &a, dim3 grid, int ring, size_t lds, hipStream_t s) {
+// block: threads per workgroup, WGS or (units) fewer.
+template <class T, int MT, int G, int S, bool FUSED, int WGS, int PAIRS = 0>
+hipError_t launch_r(const GemvArgs &a, dim3 grid, int ring, size_t lds, hipStream_t s, unsigned block = WGS) {
     if constexpr (MT == 1 && G != 32) {
         // Strip pairs stop at 4 steps (8 tiles): measured slower with 8 (Llama-3.2-1B gate_up at 512 waves:
         // 7.2 us against 6.6).
         constexpr int deep = S == 2 ? 4 : 8;
         switch (ring) {
         case 3:
-            return launch_w<T, MT, G, S, FUSED, WGS, 3>(a, grid, lds, s);
+            return launch_w<T, MT, G, S, FUSED, WGS, 3, PAIRS>(a, grid, lds, s, block);
         case 8:
-            return launch_w<T, MT, G, S, FUSED, WGS, deep>(a, grid, lds, s);
+            return launch_w<T, MT, G, S, FUSED, WGS, deep, PAIRS>(a, grid, lds, s, block);
         default:
-            return launch_w<T, MT, G, S, FUSED, WGS, 4>(a, grid, lds, s);
+            return launch_w<T, MT, G, S, FUSED, WGS, 4, PAIRS>(a, grid, lds, s, block);
         }
     } else {
-        return launch_w<T, MT, G, S, FUSED, WGS, 0>(a, grid, lds, s);
+        return launch_w<T, MT, G, S, FUSED, WGS, 0, PAIRS>(a, grid, lds, s, block);
     }
 }
 
 template <class T, int MT, int G, int S, bool FUSED>
 hipError_t launch_s(const GemvArgs &a, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
+    if constexpr (MT == 1 && FUSED) {
+        if (a.units > 0) { // `units` waves of the 16-wave instantiation
+            return launch_r<T, MT, G, S, FUSED, 1024, kUnitsOut>(a, grid, ring, lds, s, 64u * static_cast<unsigned>(a.units));
+        }
+    }
+    if constexpr (MT == 1 && !FUSED && S == 1) {
+        if (a.pair_units > 0) {
+            switch (waves) {
+            case 4:
+                return launch_r<T, MT, G, S, FUSED, 256, kUnitsIn>(a, grid, ring, lds, s);
+            case 8:
+                return launch_r<T, MT, G, S, FUSED, 512, kUnitsIn>(a, grid, ring, lds, s);
+            default:
+                return launch_r<T, MT, G, S, FUSED, 1024, kUnitsIn>(a, grid, ring, lds, s);
+            }
+        }
+    }
+    if (a.units > 0 || a.pair_units > 0) {
+        return hipErrorInvalidConfiguration;
+    }
     switch (waves) {
     case 4:
         return launch_r<T, MT, G, S, FUSED, 256>(a, grid, ring, lds, s);
@@ -828,6 +946,11 @@ GemvPlan plan_gemv(const GemvCall &c) {
         while (p.wps < 8 && p.kt_per_split >= 2 * min_run * p.wps) {
             p.wps *= 2;
         }
+        // Strip pairs whose four-wave workgroups would leave CUs idle split K in two anyway (Llama-3.2-1B
+        // gate_up: 512 pairs, 16 tiles; 256 workgroups of two pairs measured 6.0 us against 7.0 us for 128 of four).
+        if (c.fused && p.wps == 1 && p.kt_per_split >= 16 && p.groups < 4 * cus) {
+            p.wps = 2;
+        }
         while (p.nu * p.wps < 4) {
             p.nu *= 2;
         }
@@ -835,6 +958,18 @@ GemvPlan plan_gemv(const GemvCall &c) {
         // run one round on fewer CUs: measured 11.2 µs against 12.1 µs for 320 workgroups.
         if (!c.fused && p.groups > cus && p.groups < 2 * cus && p.nu * p.wps <= 8) {
             p.nu *= 2;
+        }
+        // Units: given a spill for the pairs it may split, a fused call deals its (pair, K half) units evenly over
+        // the CUs, ceil(2 pairs / CUs) waves per workgroup, where whole pairs per workgroup leave CUs with
+        // unequal work (Llama-3-8B gate_up: 896 pairs in 448 workgroups of two put four pairs on 192 CUs and
+        // two on the rest; seven halves on every CU measured 12.1 us against 12.9 us).
+        if (c.fused && c.pair_spill != nullptr && p.splits == 1 && p.wps <= 2 && c.kt_count >= 2) {
+            const int64_t u = (2 * p.groups + cus - 1) / cus;
+            if (u >= 4 && u <= 16) {
+                p.units = static_cast<int>(u);
+                p.wps = 2;
+                p.nu = 1;
+            }
         }
     } else {
         // Several rows: the launch shape (K splits, waves per strip group, strip groups per workgroup) of least
@@ -899,15 +1034,23 @@ GemvPlan plan_gemv(const GemvCall &c) {
             p.nu = 4;
         }
     }
-    p.waves = p.nu * p.wps;
+    p.waves = p.units > 0 ? p.units : p.nu * p.wps;
     const size_t stage = stage_bytes(p.kt_per_split);
     const size_t red = c.m == 1 ? static_cast<size_t>(p.waves) * p.spw * 16 * sizeof(float) : rows_red(p.wps, p.nu);
     // One row: the staging, the RMSNorm's four partial sums, then the cross-wave sums; several rows: the sums
     // reuse the staging space.
     const size_t stage16 = (stage + 15) & ~static_cast<size_t>(15);
     p.lds = c.m == 1 ? stage16 + 16 + red : std::max(stage16, red);
+    if (c.m == 1 && c.pair_units > 0) { // the split's split pairs' formed columns, 32 bytes a pair
+        p.lds += static_cast<size_t>(32 * (p.kt_per_split * 8 / c.pair_units + 1));
+    }
     p.partial_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * c.m * strips * 16 * sizeof(float) : 0;
     return p;
+}
+
+size_t gemv_pair_spill_bytes(int64_t channels) {
+    // Split pairs are pairs U j + (U - 1) / 2 for odd U >= 5: at most pairs / 5 + 1, 64 floats each.
+    return static_cast<size_t>(channels / 16 / 5 + 1) * 64 * sizeof(float);
 }
 
 size_t gemv_partial_bound(const GemvCall &c) {
@@ -942,14 +1085,17 @@ GemvArgs make_args(const GemvCall &c, const GemvPlan &p) {
     a.norm_w = c.norm_w;
     a.norm_eps = c.norm_eps;
     a.accumulate = c.accumulate;
+    a.units = p.units;
+    a.pair_units = c.pair_units;
+    a.pair_spill = c.pair_spill;
     return a;
 }
 
 hipError_t launch_args(const GemvArgs &a, const GemvCall &c, const GemvPlan &p, unsigned splits, hipStream_t stream) {
-    if (p.waves != 4 && p.waves != 8 && p.waves != 16) {
+    if (p.units > 0 ? (p.units > 16 || p.wps != 2 || splits != 1) : (p.waves != 4 && p.waves != 8 && p.waves != 16)) {
         return hipErrorInvalidConfiguration;
     }
-    const dim3 grid(static_cast<unsigned>((p.groups + p.nu - 1) / p.nu), splits);
+    const dim3 grid(static_cast<unsigned>(p.units > 0 ? (2 * p.groups + p.units - 1) / p.units : (p.groups + p.nu - 1) / p.nu), splits);
     const int group = static_cast<int>(c.w.group);
     const int ring = ring_depth(static_cast<int64_t>(grid.x) * grid.y * p.waves);
     return c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, ring, p.lds, stream)
@@ -959,6 +1105,9 @@ hipError_t launch_args(const GemvArgs &a, const GemvCall &c, const GemvPlan &p, 
 } // namespace
 
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
+    if (c.pair_units != 0 && (c.m != 1 || c.fused || c.pair_units < 0 || c.pair_units % 2 == 0 || c.pair_spill == nullptr)) {
+        return hipErrorInvalidValue;
+    }
     const GemvPlan p = plan_gemv(c);
     const GemvArgs a = make_args(c, p);
     const hipError_t e = launch_args(a, c, p, static_cast<unsigned>(p.splits), stream);

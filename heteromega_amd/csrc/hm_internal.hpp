@@ -80,18 +80,30 @@ struct GemvCall {
     const uint16_t *norm_w = nullptr;
     float norm_eps = 0.0f;
     bool accumulate = false; // plain output: y = round(y + round(x W)) (residual add into y)
+    // Strip-pair spill (gemv_pair_spill_bytes(n) bytes), for a one-row fused call whose act only a following
+    // one-row plain call reads. Given one, the fused call may deal its pairs' K halves evenly over the CUs
+    // (GemvPlan::units waves per workgroup): a pair whose halves land in two workgroups writes their fp32 sums here
+    // and leaves its act columns unwritten. The plain call over that act then passes the same spill and
+    // pair_units = the fused plan's units (when odd; even units split no pair) and forms those columns itself.
+    float *pair_spill = nullptr;
+    int pair_units = 0;
 };
 // Launch shape of a GemvCall: strips per wave, strip groups, K split, waves per strip group, strip groups per
-// workgroup, LDS bytes and the fp32 partial buffer the split needs (0 without a split).
+// workgroup, LDS bytes and the fp32 partial buffer the split needs (0 without a split). units > 0: the one-row
+// fused launch of (pair, K half) units, `units` waves per workgroup.
 struct GemvPlan {
     int spw = 1;
     int64_t groups = 0;
     int64_t splits = 1, kt_per_split = 0;
     int wps = 1, nu = 1, waves = 4;
+    int units = 0;
     size_t lds = 0;
     size_t partial_bytes = 0;
 };
 GemvPlan plan_gemv(const GemvCall &c);
+constexpr size_t kGemvLdsMax = 160 * 1024; // LDS of one workgroup
+// Bytes of the strip-pair spill of a one-row fused call over `channels` channels.
+size_t gemv_pair_spill_bytes(int64_t channels);
 // The largest partial buffer of a call like c over any range of c's columns (narrower ranges split K more).
 size_t gemv_partial_bound(const GemvCall &c);
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream);
