@@ -135,13 +135,6 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds
 #endif
 }
 
-// 4 bytes per lane, the same way (buffer_load_dword ... lds): 256 bytes to lds + 4 * lane.
-__device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4, voff, soff, 0, 0);
-#endif
-}
-
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations and is a compiler memory
 // barrier, but unlike __syncthreads() it does not wait for the wave's outstanding global loads (the
 // workgroup-scope fence of __syncthreads() waits for vmcnt(0)).
