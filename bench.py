@@ -201,7 +201,8 @@ def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0, 
     """Seconds per decode step (one FFN layer pass), cycling through the weight sets.
 
     The timed region is exactly `steps` passes: one HIP graph of `steps` passes, replayed once, wall-clocked with
-    a synchronize on both sides (after `warmup` untimed passes and warm_seconds of untimed replays). With blocks > 0
+    a synchronize on both sides (after `warmup` untimed passes, warm_seconds of untimed replays and one untimed
+    replay of the timed graph itself). With blocks > 0
     also the median per pass over `blocks` event-timed replays of a graph of BLOCK passes (BASELINE's method: HIP
     events, median). Returns (wall seconds per step, median seconds per step or None, graph of BLOCK passes, buffers)."""
     x = torch.randn((m, h), device=dev).to(layers[0].dtype)
@@ -224,6 +225,9 @@ def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0, 
     while time.perf_counter() < t_end:
         g_block.replay()
         torch.cuda.synchronize()
+    # The timed graph's own first replay carries one-time costs (measured: a 20-pass graph's first replay runs
+    # 0.5-6 us per pass slower than its later ones); it runs untimed, so the timed replay is a steady one.
+    g_timed.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     g_timed.replay()
@@ -585,8 +589,9 @@ def main():
         "config": {"workload": "Llama-3-8B SwiGLU FFN layer decode, M=1, H=4096, I=14336, W4A16 group 128, fp16 activations",
                    "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4), "weight_sets_rotated": args.sets,
                    "bytes_per_step": nbytes,
-                   "timing": "the timed steps as one HIP graph replay of exactly `steps` layer passes, wall clock with synchronize "
-                             "on both sides; the event median over blocks of 48 passes is in extra"},
+                   "timing": "the timed steps as one HIP graph replay of exactly `steps` layer passes (after an untimed replay "
+                             "of the same graph), wall clock with synchronize on both sides; the event median over blocks of 48 "
+                             "passes is in extra"},
         "roofline": out["roofline"],
         "roofline_prefill": out.get("roofline_prefill"),
         "cpu_baseline": cpu,
