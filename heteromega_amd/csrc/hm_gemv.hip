@@ -454,7 +454,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
     };
     // x's chunk c8 of the split, or its formed chunk when it belongs to a split pair. pr / pu as the high word of
-    // pr ceil(2^32 / pu): exact for pr < 2^28 (pu <= 16).
+    // pr ceil(2^32 / pu): exact for 2 <= pu <= 16 and pr < 2^24 (checked exhaustively; pairs of x number K / 16).
     const uint32_t pu_inv = forms ? 0xFFFFFFFFu / static_cast<uint32_t>(pu) + 1u : 0u;
     auto x_chunk = [&](int c8, uint4 v) {
         if constexpr (forms) {
@@ -1105,7 +1105,10 @@ hipError_t launch_args(const GemvArgs &a, const GemvCall &c, const GemvPlan &p, 
 } // namespace
 
 hipError_t launch_gemv(const GemvCall &c, hipStream_t stream) {
-    if (c.pair_units != 0 && (c.m != 1 || c.fused || c.pair_units < 0 || c.pair_units % 2 == 0 || c.pair_spill == nullptr)) {
+    // A consumer of pair units takes the odd counts a fused plan makes (5..15; its index arithmetic divides by the
+    // count as a multiply-high, exact for 2..16).
+    if (c.pair_units != 0 && (c.m != 1 || c.fused || c.pair_units < 5 || c.pair_units > 15 || c.pair_units % 2 == 0 ||
+                              c.pair_spill == nullptr)) {
         return hipErrorInvalidValue;
     }
     const GemvPlan p = plan_gemv(c);
