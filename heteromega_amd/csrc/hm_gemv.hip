@@ -270,7 +270,10 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     // as round(SiLU(g0 + g1) * (u0 + u1)), the rounding of the producer's other pairs, into the LDS area `formed`
     // (the split's split pairs in order, 16 columns each), which the staging reads in place of x.
     constexpr bool forms = PAIRS == kUnitsIn;
-    constexpr int kFormPre = 4; // columns per lane loaded ahead (a range with more forms the rest after)
+    // Columns per lane loaded ahead: 16 split pairs, what a wave's range holds when the down GEMV runs 8 waves
+    // per strip (a range of R pairs holds at most R / U + 1, and R is about 16 U there: the Llama-3-8B layer
+    // gives 16); a longer range forms the rest after, each load waited for in turn.
+    constexpr int kFormPre = 4;
     const int pu = forms ? a.pair_units : 1;
     const int phalf = (pu - 1) >> 1;
     const int cb = static_cast<int>(xk0 >> 3);                       // x chunk of the split's first K

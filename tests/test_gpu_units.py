@@ -43,6 +43,9 @@ def _units(inter_channels):
     (4096, 17408, 32, "fp16", None),              # 9, groups of 32
     (4096, 14336, 128, "fp16", (2048, 11264)),    # a channel range of 9216: 5
     (5120, 13824, 64, "bf16", None),              # Qwen2.5-14B: 7 (whole pairs kept: two down strip groups)
+    (4096, 21504, 128, "fp16", None),             # 11
+    (4096, 25600, 64, "bf16", None),              # 13
+    (4096, 29696, 128, "fp16", None),             # 15: down waves forming 16 pairs (256 columns)
 ])
 def test_forward_equals_separate_calls(oracle, hm, device, hidden, inter, group, dtype, channels):
     layer, _ = _layer(oracle, hm, device, hidden, inter, group, dtype, 31)
