@@ -64,3 +64,24 @@ def test_multirow_fused_gate_up(oracle, hm, device, m):
     up = x64 @ oracle.weights_f64(*up_np, g, dtype)
     ref = oracle.silu(gate) * up
     assert_close(oracle, host_f64(act), ref, dtype, f"gate_up M={m}")
+
+
+@pytest.mark.parametrize("m", [2, 5, 8, 16])
+@pytest.mark.parametrize("hidden,inter,group,dtype", [
+    (4096, 14336, 128, "fp16"),   # Llama-3-8B: the down GEMV splits K at every row count
+    (5120, 13824, 64, "bf16"),    # Qwen2.5-14B
+    (2048, 8192, 128, "fp16"),    # Llama-3.2-1B
+])
+def test_forward_equals_separate_calls(oracle, hm, device, m, hidden, inter, group, dtype):
+    # hm_ffn_forward at 2..16 rows against hm_ffn_gate_up then hm_ffn_down on the caller's act: the same bits,
+    # including the down GEMV's K-split partials and their sum, on two calls in a row over one workspace.
+    rng = np.random.default_rng(1000 + m + hidden)
+    ws = [oracle.random_weights(rng, k, n, group, dtype) for k, n in ((hidden, inter), (hidden, inter), (inter, hidden))]
+    ffn = hm.FfnLayer.from_logical(*(logical_to_device(w, dtype, device) for w in ws), group, dtype=TORCH[dtype])
+    print(f"forward M={m} [{hidden} x {inter}] g={group} {dtype}", flush=True)
+    for rep in range(2):
+        _, x = make_x(oracle, rng, m, hidden, dtype, device)
+        y = ffn.forward(x)
+        ref = ffn.down(ffn.gate_up(x))
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), (m, hidden, dtype, rep)
