@@ -46,6 +46,9 @@ def _units(inter_channels):
     (4096, 21504, 128, "fp16", None),             # 11
     (4096, 25600, 64, "bf16", None),              # 13
     (4096, 29696, 128, "fp16", None),             # 15: down waves forming 16 pairs (256 columns)
+    (3968, 9216, 128, "fp16", None),              # 5, 31 K tiles: halves of 16 and 15
+    (3968, 14336, 32, "bf16", None),              # 7, 31 K tiles, groups of 32
+    (6144, 14336, 32, "bf16", None),              # 7, but two down strip groups per workgroup: whole pairs
 ])
 def test_forward_equals_separate_calls(oracle, hm, device, hidden, inter, group, dtype, channels):
     layer, _ = _layer(oracle, hm, device, hidden, inter, group, dtype, 31)
