@@ -294,8 +294,8 @@ def measured_traffic():
 
 def pmc_probe(hm, torch, dev, H, I, G, sets, rows=1):
     """Eager launches for one rocprofv3 --pmc pass: a copy kernel of known size (calibration), then the fused
-    gate_up GEMV and the down GEMV of the headline workload (or of the same layer at `rows` rows), on rotating
-    weight sets."""
+    gate_up GEMV and the down GEMV of the headline workload (or of the same layer at `rows` rows), then the layer's
+    forward (whose one-row kernels are the pair-unit builds), on rotating weight sets."""
     words = (64 << 20) // 4
     bufs = [torch.empty(words, dtype=torch.int32, device=dev).random_(0, 1 << 30) for _ in range(4)]
     outs = [torch.empty_like(b) for b in bufs]
@@ -317,6 +317,12 @@ def pmc_probe(hm, torch, dev, H, I, G, sets, rows=1):
         layers[r % sets].down(act, y)
     torch.cuda.synchronize()
     log(f"pmc probe: {2 * sets} down launches (M={rows})")
+    ws = layers[0].workspace(rows)
+    for r in range(2 * sets):
+        layers[r % sets].forward(x, y, workspace=ws)
+    torch.cuda.synchronize()
+    log(f"pmc probe: {2 * sets} layer forwards (M={rows}; at one row the pair-unit gate_up and the down GEMV that "
+        f"forms its split pairs)")
 
 
 def host_cpus():
