@@ -88,6 +88,10 @@ _SIGNATURES = {
     "hm_rmsnorm": (ctypes.c_int, [P, I64, P, I64, P, I64, I64, ctypes.c_float, ctypes.c_int, P]),
     "hm_residual_add2": (ctypes.c_int, [P, I64, P, I64, P, I64, I64, I64, ctypes.c_int, P]),
     "hm_residual_rmsnorm": (ctypes.c_int, [P, I64, P, I64, P, P, I64, I64, I64, ctypes.c_float, ctypes.c_int, P]),
+    "hm_residual2_rmsnorm": (ctypes.c_int, [P, I64, P, I64, P, I64, P, P, I64, I64, I64, ctypes.c_float, ctypes.c_int, P]),
+    "hm_residual_add2_mixed": (ctypes.c_int, [P, I64, P, I64, I32, P, I64, I32, I64, I64, ctypes.c_int, P]),
+    "hm_find_nonfinite": (I64, [P, I64, I64, I64, ctypes.c_int, I32]),
+    "hm_find_nonfinite_device": (ctypes.c_int, [P, I64, I64, I64, ctypes.c_int, I32, P, P]),
     "hm_partition_check": (ctypes.c_int, [I64, I64, I64]),
     "hm_partition_from_ratio": (ctypes.c_int, [I64, ctypes.c_double, I64, ctypes.POINTER(I64)]),
     "hm_split_type": (I32, [I32, I32, I32, I32, I32, I32]),

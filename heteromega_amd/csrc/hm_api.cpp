@@ -1192,10 +1192,78 @@ hm_status hm_residual_rmsnorm(void *x, int64_t ldx, const void *y, int64_t ldy, 
         !aligned(normed, 16) || !(eps >= 0.0f)) {
         return fail(HM_INVALID_ARGUMENT, "hm_residual_rmsnorm: rows of a multiple of 8 columns, 16-byte aligned, eps >= 0");
     }
-    const hipError_t e = hm::launch_residual_rmsnorm(static_cast<uint16_t *>(x), ldx, static_cast<const uint16_t *>(y), ldy,
+    const hipError_t e = hm::launch_residual_rmsnorm(static_cast<uint16_t *>(x), ldx, static_cast<const uint16_t *>(y), ldy, nullptr, 0,
                                                      static_cast<const uint16_t *>(weight), static_cast<uint16_t *>(normed), ld_normed, rows,
                                                      cols, eps, dtype, as_stream(stream));
     return e == hipSuccess ? HM_OK : hip_fail(e, "residual_rmsnorm launch");
+}
+
+hm_status hm_residual2_rmsnorm(void *x, int64_t ldx, const void *a, int64_t lda, const void *b, int64_t ldb, const void *weight, void *normed,
+                               int64_t ld_normed, int64_t rows, int64_t cols, float eps, hm_dtype dtype, void *stream) {
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    if (x == nullptr || weight == nullptr || normed == nullptr || rows < 0 || cols <= 0 || cols % 8 || ldx % 8 || ld_normed % 8 ||
+        ldx < cols || ld_normed < cols || !aligned(x, 16) || !aligned(weight, 16) || !aligned(normed, 16) || !(eps >= 0.0f) ||
+        (a != nullptr && (lda % 8 || lda < cols || !aligned(a, 16))) || (a != nullptr && b != nullptr && (ldb % 8 || ldb < cols || !aligned(b, 16)))) {
+        return fail(HM_INVALID_ARGUMENT, "hm_residual2_rmsnorm: rows of a multiple of 8 columns, 16-byte aligned, eps >= 0");
+    }
+    const hipStream_t s = as_stream(stream);
+    // Without a, x stays as it is (b is not read) and the call is the plain RMSNorm.
+    const hipError_t e =
+        a == nullptr ? hm::launch_rmsnorm(static_cast<uint16_t *>(normed), ld_normed, static_cast<const uint16_t *>(x), ldx,
+                                          static_cast<const uint16_t *>(weight), rows, cols, eps, dtype, s)
+                     : hm::launch_residual_rmsnorm(static_cast<uint16_t *>(x), ldx, static_cast<const uint16_t *>(a), lda,
+                                                   static_cast<const uint16_t *>(b), ldb, static_cast<const uint16_t *>(weight),
+                                                   static_cast<uint16_t *>(normed), ld_normed, rows, cols, eps, dtype, s);
+    return e == hipSuccess ? HM_OK : hip_fail(e, "residual2_rmsnorm launch");
+}
+
+hm_status hm_residual_add2_mixed(void *x, int64_t ldx, const void *a, int64_t lda, int32_t a_fp32, const void *b, int64_t ldb, int32_t b_fp32,
+                                 int64_t rows, int64_t cols, hm_dtype dtype, void *stream) {
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    if (x == nullptr || a == nullptr || b == nullptr || rows < 0 || cols <= 0 || cols % 8 || ldx % 8 || lda % 8 || ldb % 8 || ldx < cols ||
+        lda < cols || ldb < cols || !aligned(x, 16) || !aligned(a, 16) || !aligned(b, 16)) {
+        return fail(HM_INVALID_ARGUMENT, "hm_residual_add2_mixed: x, a and b rows of a multiple of 8 columns, 16-byte aligned");
+    }
+    const hipError_t e = hm::launch_residual_add2_mixed(static_cast<uint16_t *>(x), ldx, a, lda, a_fp32 != 0, b, ldb, b_fp32 != 0, rows, cols,
+                                                        dtype, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "residual_add2_mixed launch");
+}
+
+int64_t hm_find_nonfinite(const void *bits, int64_t rows, int64_t cols, int64_t ld, hm_dtype dtype, int32_t sampled) {
+    if (bits == nullptr || rows <= 0 || cols <= 0 || ld < cols || check_dtype(dtype) != HM_OK) {
+        return -1;
+    }
+    const uint16_t mask = dtype == HM_FP16 ? 0x7C00u : 0x7F80u;
+    const int64_t stride = sampled ? HM_FINITE_SAMPLE_STRIDE : 1;
+    const uint16_t *p = static_cast<const uint16_t *>(bits);
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t c = 0; c < cols; c += stride) {
+            if ((p[r * ld + c] & mask) == mask) {
+                return r * cols + c;
+            }
+        }
+    }
+    return -1;
+}
+
+hm_status hm_find_nonfinite_device(const void *x, int64_t rows, int64_t cols, int64_t ld, hm_dtype dtype, int32_t sampled, int64_t *first,
+                                   void *stream) {
+    hm_status st = check_dtype(dtype);
+    if (st != HM_OK) {
+        return st;
+    }
+    if (x == nullptr || first == nullptr || rows < 0 || cols <= 0 || ld < cols || !aligned(first, 8)) {
+        return fail(HM_INVALID_ARGUMENT, "hm_find_nonfinite_device: x [rows, cols] with ld >= cols and an 8-byte aligned device int64");
+    }
+    const hipError_t e = hm::launch_find_nonfinite(static_cast<const uint16_t *>(x), ld, rows, cols, sampled ? HM_FINITE_SAMPLE_STRIDE : 1,
+                                                   dtype, first, as_stream(stream));
+    return e == hipSuccess ? HM_OK : hip_fail(e, "find_nonfinite launch");
 }
 
 hm_status hm_partition_check(int64_t intermediate, int64_t npu_channels, int64_t alignment) {

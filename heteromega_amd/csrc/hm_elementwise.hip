@@ -16,6 +16,13 @@ template <class T> __device__ __forceinline__ void load8(const uint16_t *p, floa
     }
 }
 
+// Eight fp32 partials (two 16-byte loads).
+__device__ __forceinline__ void load8_f32(const float *p, float o[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p);
+    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+    o[0] = a.x, o[1] = a.y, o[2] = a.z, o[3] = a.w, o[4] = b.x, o[5] = b.y, o[6] = b.z, o[7] = b.w;
+}
+
 template <class T> __device__ __forceinline__ void store8(uint16_t *p, const float v[8]) {
     uint4 o;
     uint32_t *w = reinterpret_cast<uint32_t *>(&o);
@@ -75,9 +82,12 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
 // trip and x is not read back after its residual update.
 constexpr int kCached = 4;
 
+// With a second addend zr (may be null): x = round((x + y) + z), the order of the reference's residual_norm
+// (kernels/gpu/src/residual_norm.cu:45-49).
 template <class T, bool ADD>
 __device__ __forceinline__ void rmsnorm_cached(uint16_t *__restrict__ out, uint16_t *__restrict__ xr, const uint16_t *__restrict__ yr,
-                                               const uint16_t *__restrict__ w, int64_t cols, float eps, float *scratch) {
+                                               const uint16_t *__restrict__ zr, const uint16_t *__restrict__ w, int64_t cols, float eps,
+                                               float *scratch) {
     float v[kCached][8], g[kCached][8];
     float ss = 0.0f;
 #pragma unroll
@@ -89,9 +99,18 @@ __device__ __forceinline__ void rmsnorm_cached(uint16_t *__restrict__ out, uint1
             if constexpr (ADD) {
                 float a[8];
                 load8<T>(yr + c, a);
+                if (zr != nullptr) {
+                    float b[8];
+                    load8<T>(zr + c, b);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    v[j][k] = T::to_float(T::from_float(v[j][k] + a[k]));
+                    for (int k = 0; k < 8; ++k) {
+                        v[j][k] = T::to_float(T::from_float((v[j][k] + a[k]) + b[k]));
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        v[j][k] = T::to_float(T::from_float(v[j][k] + a[k]));
+                    }
                 }
                 store8<T>(xr + c, v[j]);
             }
@@ -119,13 +138,14 @@ __device__ __forceinline__ void rmsnorm_cached(uint16_t *__restrict__ out, uint1
 
 template <class T, bool ADD>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(uint16_t *__restrict__ out, int64_t ld_out, uint16_t *__restrict__ x, int64_t ldx,
-                                                      const uint16_t *__restrict__ y, int64_t ldy, const uint16_t *__restrict__ w,
-                                                      int64_t cols, float eps) {
+                                                      const uint16_t *__restrict__ y, int64_t ldy, const uint16_t *__restrict__ z,
+                                                      int64_t ldz, const uint16_t *__restrict__ w, int64_t cols, float eps) {
     __shared__ float scratch[4];
     const int64_t r = blockIdx.x;
     uint16_t *xr = x + r * ldx;
     if (cols <= kCached * 2048) {
-        rmsnorm_cached<T, ADD>(out + r * ld_out, xr, ADD ? y + r * ldy : nullptr, w, cols, eps, scratch);
+        rmsnorm_cached<T, ADD>(out + r * ld_out, xr, ADD ? y + r * ldy : nullptr, ADD && z != nullptr ? z + r * ldz : nullptr, w, cols, eps,
+                               scratch);
         return;
     }
     float ss = 0.0f;
@@ -135,9 +155,18 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(uint16_t *__restrict__ out
         if constexpr (ADD) {
             float a[8];
             load8<T>(y + r * ldy + c, a);
+            if (z != nullptr) {
+                float b[8];
+                load8<T>(z + r * ldz + c, b);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                v[k] = T::to_float(T::from_float(v[k] + a[k]));
+                for (int k = 0; k < 8; ++k) {
+                    v[k] = T::to_float(T::from_float((v[k] + a[k]) + b[k]));
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    v[k] = T::to_float(T::from_float(v[k] + a[k]));
+                }
             }
             store8<T>(xr + c, v);
         }
@@ -194,6 +223,64 @@ __global__ void __launch_bounds__(256) residual_add2_kernel(uint16_t *__restrict
     }
 }
 
+// x += a + b with each partial 16-bit (the activation type) or fp32 (the reference's residual_add2 takes either,
+// kernels/gpu/src/residual_add.cu:9-31): the partials are added first, then the residual, one rounding.
+template <class T, bool A32, bool B32>
+__global__ void __launch_bounds__(256) residual_add2_mixed_kernel(uint16_t *__restrict__ x, int64_t ldx, const void *__restrict__ a, int64_t lda,
+                                                                  const void *__restrict__ b, int64_t ldb, int64_t rows, int64_t cols) {
+    const int64_t per_row = cols / 8;
+    const int64_t total = rows * per_row;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t r = i / per_row;
+        const int64_t c = (i - r * per_row) * 8;
+        float v[8], t[8], u[8];
+        load8<T>(x + r * ldx + c, v);
+        if constexpr (A32) {
+            load8_f32(static_cast<const float *>(a) + r * lda + c, t);
+        } else {
+            load8<T>(static_cast<const uint16_t *>(a) + r * lda + c, t);
+        }
+        if constexpr (B32) {
+            load8_f32(static_cast<const float *>(b) + r * ldb + c, u);
+        } else {
+            load8<T>(static_cast<const uint16_t *>(b) + r * ldb + c, u);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            v[k] += t[k] + u[k];
+        }
+        store8<T>(x + r * ldx + c, v);
+    }
+}
+
+// Nonfinite scan: 8 elements per thread, element (r, c) checked for c < cols (all) or c % stride == 0 (sampled);
+// the least row-major index r * cols + c of a nonfinite one goes to *first by an unsigned atomic min. *first starts
+// at kNoIndex (find_init, a kernel rather than a memset so that the scan can be captured in a graph), which read as
+// an int64 is -1, the answer when nothing is found.
+constexpr unsigned long long kNoIndex = ~0ull;
+__global__ void find_init(unsigned long long *first) { *first = kNoIndex; }
+template <bool FP16>
+__global__ void __launch_bounds__(256) find_nonfinite_kernel(const uint16_t *__restrict__ x, int64_t ld, int64_t rows, int64_t cols, int64_t stride,
+                                                             unsigned long long *first) {
+    const uint32_t mask = FP16 ? 0x7C00u : 0x7F80u;
+    const int64_t per_row = (cols + 8 * stride - 1) / (8 * stride); // groups of 8 checked elements per row
+    const int64_t total = rows * per_row;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t r = i / per_row;
+        const int64_t c0 = (i - r * per_row) * 8 * stride;
+        unsigned long long hit = kNoIndex;
+        for (int k = 7; k >= 0; --k) { // highest first, so the least index is kept
+            const int64_t c = c0 + k * stride;
+            if (c < cols && (x[r * ld + c] & mask) == mask) {
+                hit = static_cast<unsigned long long>(r * cols + c);
+            }
+        }
+        if (hit != kNoIndex) {
+            atomicMin(first, hit);
+        }
+    }
+}
+
 dim3 grid_for(int64_t work) {
     const int64_t blocks = (work + 255) / 256;
     return dim3(static_cast<unsigned>(blocks < 8192 ? (blocks > 0 ? blocks : 1) : 8192));
@@ -223,25 +310,58 @@ hipError_t launch_rmsnorm(uint16_t *out, int64_t ld_out, const uint16_t *x, int6
     uint16_t *xm = const_cast<uint16_t *>(x); // not written without ADD
     if (dtype == 1) {
         hipLaunchKernelGGL((rmsnorm_kernel<F16, false>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, out, ld_out, xm, ldx,
-                           static_cast<const uint16_t *>(nullptr), int64_t(0), weight, cols, eps);
+                           static_cast<const uint16_t *>(nullptr), int64_t(0), static_cast<const uint16_t *>(nullptr), int64_t(0), weight, cols,
+                           eps);
     } else {
         hipLaunchKernelGGL((rmsnorm_kernel<BF16, false>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, out, ld_out, xm, ldx,
-                           static_cast<const uint16_t *>(nullptr), int64_t(0), weight, cols, eps);
+                           static_cast<const uint16_t *>(nullptr), int64_t(0), static_cast<const uint16_t *>(nullptr), int64_t(0), weight, cols,
+                           eps);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_residual_rmsnorm(uint16_t *x, int64_t ldx, const uint16_t *y, int64_t ldy, const uint16_t *weight, uint16_t *normed,
-                                   int64_t ld_normed, int64_t rows, int64_t cols, float eps, int dtype, hipStream_t stream) {
+hipError_t launch_residual_rmsnorm(uint16_t *x, int64_t ldx, const uint16_t *y, int64_t ldy, const uint16_t *z, int64_t ldz,
+                                   const uint16_t *weight, uint16_t *normed, int64_t ld_normed, int64_t rows, int64_t cols, float eps, int dtype,
+                                   hipStream_t stream) {
     if (rows == 0) {
         return hipSuccess;
     }
     if (dtype == 1) {
         hipLaunchKernelGGL((rmsnorm_kernel<F16, true>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, normed, ld_normed, x, ldx, y,
-                           ldy, weight, cols, eps);
+                           ldy, z, ldz, weight, cols, eps);
     } else {
         hipLaunchKernelGGL((rmsnorm_kernel<BF16, true>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, normed, ld_normed, x, ldx,
-                           y, ldy, weight, cols, eps);
+                           y, ldy, z, ldz, weight, cols, eps);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_residual_add2_mixed(uint16_t *x, int64_t ldx, const void *a, int64_t lda, bool a32, const void *b, int64_t ldb, bool b32,
+                                      int64_t rows, int64_t cols, int dtype, hipStream_t stream) {
+    const int64_t work = rows * (cols / 8);
+    if (work == 0) {
+        return hipSuccess;
+    }
+    const dim3 g = grid_for(work);
+    auto kern = dtype == 1 ? (a32 ? (b32 ? residual_add2_mixed_kernel<F16, true, true> : residual_add2_mixed_kernel<F16, true, false>)
+                                  : (b32 ? residual_add2_mixed_kernel<F16, false, true> : residual_add2_mixed_kernel<F16, false, false>))
+                           : (a32 ? (b32 ? residual_add2_mixed_kernel<BF16, true, true> : residual_add2_mixed_kernel<BF16, true, false>)
+                                  : (b32 ? residual_add2_mixed_kernel<BF16, false, true> : residual_add2_mixed_kernel<BF16, false, false>));
+    hipLaunchKernelGGL(kern, g, dim3(256), 0, stream, x, ldx, a, lda, b, ldb, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_find_nonfinite(const uint16_t *x, int64_t ld, int64_t rows, int64_t cols, int64_t stride, int dtype, int64_t *first,
+                                 hipStream_t stream) {
+    unsigned long long *f = reinterpret_cast<unsigned long long *>(first);
+    hipLaunchKernelGGL(find_init, dim3(1), dim3(1), 0, stream, f);
+    const int64_t work = rows * ((cols + 8 * stride - 1) / (8 * stride));
+    if (work > 0) {
+        if (dtype == 1) {
+            hipLaunchKernelGGL(find_nonfinite_kernel<true>, grid_for(work), dim3(256), 0, stream, x, ld, rows, cols, stride, f);
+        } else {
+            hipLaunchKernelGGL(find_nonfinite_kernel<false>, grid_for(work), dim3(256), 0, stream, x, ld, rows, cols, stride, f);
+        }
     }
     return hipGetLastError();
 }

@@ -153,8 +153,15 @@ hipError_t launch_rmsnorm(uint16_t *out, int64_t ld_out, const uint16_t *x, int6
                           int64_t rows, int64_t cols, float eps, int dtype, hipStream_t stream);
 hipError_t launch_residual_add2(uint16_t *x, int64_t ldx, const uint16_t *a, int64_t lda, const uint16_t *b, int64_t ldb,
                                 int64_t rows, int64_t cols, int dtype, hipStream_t stream);
-hipError_t launch_residual_rmsnorm(uint16_t *x, int64_t ldx, const uint16_t *y, int64_t ldy, const uint16_t *weight,
-                                   uint16_t *normed, int64_t ld_normed, int64_t rows, int64_t cols, float eps, int dtype,
+// x = round(x + y) (z null) or round((x + y) + z), then normed = RMSNorm(x) * weight.
+hipError_t launch_residual_rmsnorm(uint16_t *x, int64_t ldx, const uint16_t *y, int64_t ldy, const uint16_t *z, int64_t ldz,
+                                   const uint16_t *weight, uint16_t *normed, int64_t ld_normed, int64_t rows, int64_t cols, float eps, int dtype,
                                    hipStream_t stream);
+// x += a + b with a and b each 16-bit (the activation type) or fp32.
+hipError_t launch_residual_add2_mixed(uint16_t *x, int64_t ldx, const void *a, int64_t lda, bool a32, const void *b, int64_t ldb, bool b32,
+                                      int64_t rows, int64_t cols, int dtype, hipStream_t stream);
+// *first (device int64) = least row-major index r * cols + c of a nonfinite element with c % stride == 0, or -1.
+hipError_t launch_find_nonfinite(const uint16_t *x, int64_t ld, int64_t rows, int64_t cols, int64_t stride, int dtype, int64_t *first,
+                                 hipStream_t stream);
 
 } // namespace hm

@@ -368,7 +368,15 @@ def rmsnorm(out, x, weight, eps=1e-5, stream=None):
 
 
 def residual_add2(x, y_g, y_n=None, stream=None):
-    """x += y_g + y_n (heteromega::residual_add2, residual_add.cu:9-73); y_n may be None."""
+    """x += y_g + y_n (heteromega::residual_add2, residual_add.cu:9-73); y_n may be None. Each partial is of x's
+    type or float32 (then both must be given, as in the reference)."""
+    if (y_g is not None and y_g.dtype == torch.float32) or (y_n is not None and y_n.dtype == torch.float32):
+        if y_g is None or y_n is None:
+            raise ValueError("residual_add2: fp32 partials need both y_g and y_n")
+        _call(_lib.load().hm_residual_add2_mixed(_ptr(x), x.stride(0), _ptr(y_g), y_g.stride(0), int(y_g.dtype == torch.float32), _ptr(y_n),
+                                                 y_n.stride(0), int(y_n.dtype == torch.float32), x.size(0), x.size(1), _hm_dtype(x.dtype),
+                                                 _stream(stream, x.device)))
+        return x
     _call(_lib.load().hm_residual_add2(_ptr(x), x.stride(0), _ptr(y_g), y_g.stride(0) if y_g is not None else 0, _ptr(y_n),
                                        y_n.stride(0) if y_n is not None else 0, x.size(0), x.size(1), _hm_dtype(x.dtype),
                                        _stream(stream, x.device)))
@@ -380,6 +388,34 @@ def residual_rmsnorm(x, y, weight, normed, eps=1e-5, stream=None):
     _call(_lib.load().hm_residual_rmsnorm(_ptr(x), x.stride(0), _ptr(y), y.stride(0), _ptr(weight), _ptr(normed), normed.stride(0),
                                           x.size(0), x.size(1), eps, _hm_dtype(x.dtype), _stream(stream, x.device)))
     return normed
+
+
+def residual_norm(x, a, b, weight, normed, eps=1e-5, stream=None):
+    """x = round((x + a) + b), then normed = RMSNorm(x) * weight, in one dispatch (heteromega::residual_norm_bf16,
+    residual_norm.cu:25-106, without its GEMM input prep). a and b may be None; without a, x is left as it is."""
+    _call(_lib.load().hm_residual2_rmsnorm(_ptr(x), x.stride(0), _ptr(a), a.stride(0) if a is not None else 0, _ptr(b),
+                                           b.stride(0) if b is not None else 0, _ptr(weight), _ptr(normed), normed.stride(0), x.size(0),
+                                           x.size(1), eps, _hm_dtype(x.dtype), _stream(stream, x.device)))
+    return normed
+
+
+kFiniteSampleStride = 64
+
+
+def find_nonfinite(t, sampled=False, stream=None):
+    """Index of the first checked inf/NaN element of a [rows, columns] fp16/bf16 tensor, or -1: every element, or
+    every row at one in kFiniteSampleStride columns (heteromega::find_nonfinite_bf16 with FiniteCheck::kFull /
+    kSampled, merged_ffn_contract.hpp:13-39). A device tensor is scanned on the GPU where it lies (one int64
+    comes back); a host tensor on the host."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError("find_nonfinite: a [rows, columns] tensor with a contiguous last dimension")
+    L = _lib.load()
+    if t.is_cuda:
+        first = torch.empty((1,), dtype=torch.int64, device=t.device)
+        _call(L.hm_find_nonfinite_device(_ptr(t), t.size(0), t.size(1), t.stride(0), _hm_dtype(t.dtype), int(bool(sampled)), _ptr(first),
+                                         _stream(stream, t.device)))
+        return int(first.item())
+    return int(L.hm_find_nonfinite(_ptr(t), t.size(0), t.size(1), t.stride(0), _hm_dtype(t.dtype), int(bool(sampled))))
 
 
 # ---- FFN layer --------------------------------------------------------------------------------------
@@ -654,5 +690,5 @@ __all__ = [
     "HMError", "kTileK", "kTileN", "kTileBytes", "padded_rows", "packed_bytes", "packed_tile_index", "pack_w4a16",
     "awq_unpack_qweight", "awq_unpack_qzeros", "gptq_unpack_qweight", "gptq_unpack_qzeros", "RepackedMatrix", "packed_linear", "packed_linear_k_split",
     "packed_linear_swiglu", "gemv_w4a16", "gemm_w4a16", "silu_mul",
-    "rmsnorm", "residual_add2", "residual_rmsnorm", "FfnLayer", "FFNPartition", "ffn_partitioned", "ffn_row_split", "GpuFfnModel",
+    "rmsnorm", "residual_add2", "residual_rmsnorm", "residual_norm", "kFiniteSampleStride", "find_nonfinite", "FfnLayer", "FFNPartition", "ffn_partitioned", "ffn_row_split", "GpuFfnModel",
 ]

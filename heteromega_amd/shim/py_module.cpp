@@ -59,7 +59,65 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         w.packed_channels = packed_channels;
         auto buf = heteromega::GpuFfnBuffers::allocate(x_norm.size(0), w.channels(), hidden, x_norm.device());
         heteromega::gpu_ffn_slice_forward(w, x_norm, buf, y, as_stream(stream));
-        return buf.workspace; // kept alive by the caller until the stream has run the launch
+        // kept alive by the caller until the stream has run the launch
+        return pybind11::make_tuple(buf.gate_up, buf.act, buf.x_pad, buf.workspace.defined() ? buf.workspace : torch::Tensor());
+    });
+    m.def("pack_w4a16", &heteromega::pack_w4a16);
+    m.def("pack_ffn_slice", [](const std::vector<torch::Tensor> &t, int64_t begin, int64_t end, const std::string &layout) {
+        TORCH_CHECK(t.size() == 9, "pack_ffn_slice: gate q/s/z, up q/s/z, down q/s/z");
+        heteromega::FfnLayerQuant q{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8]};
+        const auto w = heteromega::pack_ffn_slice(q, begin, end, layout_of(layout));
+        return pybind11::make_tuple(w.gate_up, w.down, w.begin, w.end, w.hidden);
+    });
+    m.def("slice_packed_ffn", [](const torch::Tensor &gate, const torch::Tensor &up, const torch::Tensor &down, int64_t hidden, int64_t inter,
+                                 int64_t begin, int64_t end, const std::string &layout, const std::string &device) {
+        auto w = heteromega::slice_packed_ffn(gate, up, down, hidden, inter, begin, end, layout_of(layout));
+        if (!device.empty()) {
+            w = w.to(torch::Device(device));
+        }
+        return pybind11::make_tuple(w.gate_up, w.down, w.begin, w.end, w.hidden);
+    });
+    m.def("residual_add2", [](torch::Tensor x, const torch::Tensor &y_g, const torch::Tensor &y_n, uint64_t stream) {
+        heteromega::residual_add2(x, y_g, y_n, as_stream(stream));
+    });
+    m.def("residual_norm_supports", &heteromega::residual_norm_supports);
+    // Tensors stand for the reference's raw pointers (an undefined tensor for a null one). After the boundary, one
+    // gemm_w4a16 per packed [h, n] matrix in gemm_w reads gemm_x, as the reference's Q/K/V GEMMs do; returns the reuse's
+    // hits and their outputs.
+    m.def("residual_norm_bf16", [](torch::Tensor x, const std::optional<torch::Tensor> &a, const std::optional<torch::Tensor> &b,
+                                   const torch::Tensor &weight, const std::optional<torch::Tensor> &normed, torch::Tensor gemm_x, float eps,
+                                   uint64_t stream, const std::vector<torch::Tensor> &gemm_w, int64_t n) {
+        auto ptr = [](const std::optional<torch::Tensor> &t) { return t ? reinterpret_cast<uint16_t *>(t->data_ptr()) : nullptr; };
+        heteromega::GemmInputReuse reuse;
+        const int64_t m = x.size(0), h = x.size(1);
+        heteromega::residual_norm_bf16(reinterpret_cast<uint16_t *>(x.data_ptr()), ptr(a), ptr(b), reinterpret_cast<const uint16_t *>(weight.data_ptr()),
+                                       ptr(normed), gemm_x.data_ptr(), reuse, m, h, x.stride(0), a ? a->stride(0) : 0, b ? b->stride(0) : 0,
+                                       gemm_x.stride(0), eps, as_stream(stream));
+        std::vector<torch::Tensor> outs;
+        for (const auto &w : gemm_w) {
+            auto out = torch::empty({m, n}, gemm_x.options());
+            heteromega::gemm_w4a16(out, gemm_x, w, h, n, h, n, as_stream(stream));
+            outs.push_back(out);
+        }
+        return pybind11::make_tuple(reuse.hits(), outs);
+    });
+    m.def("gemm_input_buffers", [](int64_t m, int64_t k, uint64_t stream) {
+        float *sums = nullptr;
+        uint16_t *tiles = nullptr;
+        heteromega::gemm_input_buffers(m, k, as_stream(stream), &sums, &tiles);
+    });
+    m.def("configured_gemm_kernel", []() { return heteromega::configured_gemm_kernel() == heteromega::GemmKernel::kHeteroMega ? "fast" : "mosaic"; });
+    m.def("gemm_uncached_weights", &heteromega::gemm_uncached_weights);
+    m.def("parse_finite_check", [](const std::string &v, bool null) {
+        return heteromega::parse_finite_check(null ? nullptr : v.c_str()) == heteromega::FiniteCheck::kSampled ? "sampled" : "full";
+    });
+    m.def("find_nonfinite_bf16", [](const torch::Tensor &bits, bool sampled) {
+        TORCH_CHECK(bits.device().is_cpu() && bits.dim() == 2 && bits.is_contiguous() && bits.element_size() == 2, "CPU [rows, columns] 16-bit tensor");
+        return heteromega::find_nonfinite_bf16(reinterpret_cast<const uint16_t *>(bits.data_ptr()), bits.size(0), bits.size(1),
+                                               sampled ? heteromega::FiniteCheck::kSampled : heteromega::FiniteCheck::kFull);
+    });
+    m.def("find_nonfinite_device", [](const torch::Tensor &t, bool sampled, torch::Tensor first, uint64_t stream) {
+        heteromega::find_nonfinite_device(t, sampled ? heteromega::FiniteCheck::kSampled : heteromega::FiniteCheck::kFull, first, as_stream(stream));
     });
     pybind11::class_<heteromega::GpuFfnModel>(m, "GpuFfnModel")
         .def(pybind11::init<>())

@@ -313,6 +313,38 @@ hm_status hm_residual_add2(void *x, int64_t ldx, const void *a, int64_t lda, con
 hm_status hm_residual_rmsnorm(void *x, int64_t ldx, const void *y, int64_t ldy, const void *weight, void *normed,
                               int64_t ld_normed, int64_t rows, int64_t cols, float eps, hm_dtype dtype, void *stream);
 
+/* The same with two addends: x = round((x + a) + b) (b may be NULL), then normed = RMSNorm(x) * weight; with a
+ * NULL, x is left as it is and only the norm runs. Replaces heteromega::residual_norm_bf16
+ * (kernels/gpu/include/heteromega/gpu_ffn.hpp:136-141, kernels/gpu/src/residual_norm.cu:25-106) without its
+ * prepared GEMM input: the engine's GEMM reads its input rows from memory. */
+hm_status hm_residual2_rmsnorm(void *x, int64_t ldx, const void *a, int64_t lda, const void *b, int64_t ldb, const void *weight,
+                               void *normed, int64_t ld_normed, int64_t rows, int64_t cols, float eps, hm_dtype dtype,
+                               void *stream);
+
+/* x += a + b per element with each partial either in x's type (a_fp32 / b_fp32 = 0) or fp32 (1): the partials are
+ * added first, then the residual, fp32 math, one rounding. Replaces heteromega::residual_add2 with fp32 partials
+ * (kernels/gpu/include/heteromega/gpu_ffn.hpp:162-163, kernels/gpu/src/residual_add.cu:48-73). */
+hm_status hm_residual_add2_mixed(void *x, int64_t ldx, const void *a, int64_t lda, int32_t a_fp32, const void *b,
+                                 int64_t ldb, int32_t b_fp32, int64_t rows, int64_t cols, hm_dtype dtype, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Nonfinite scan (the merged FFN's failure check).
+ * ------------------------------------------------------------------------- */
+
+/* Columns between the checked ones of a sampled scan (include/heteromega/merged_ffn_contract.hpp:18). */
+#define HM_FINITE_SAMPLE_STRIDE 64
+
+/* Host memory: the least row-major index r * cols + c of an element of rows x cols 16-bit values (row stride ld)
+ * whose exponent bits are all set (inf or NaN), checking every column (sampled = 0) or every
+ * HM_FINITE_SAMPLE_STRIDE-th (sampled = 1); -1 when there is none or the arguments are invalid. Replaces
+ * heteromega::find_nonfinite_bf16 with FiniteCheck::kFull / kSampled (merged_ffn_contract.hpp:13-39) and covers fp16. */
+int64_t hm_find_nonfinite(const void *bits, int64_t rows, int64_t cols, int64_t ld, hm_dtype dtype, int32_t sampled);
+
+/* The same scan of device memory, enqueued on `stream`: *first (a device int64) receives the index or -1. No
+ * allocation and no host wait: an output can be checked where it lies, without a copy to the host. */
+hm_status hm_find_nonfinite_device(const void *x, int64_t rows, int64_t cols, int64_t ld, hm_dtype dtype, int32_t sampled,
+                                   int64_t *first, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Partition descriptor (host). The other device's share is [0, npu_channels),
  * the GPU's is [npu_channels, intermediate), as in npu/ffn/reference.py:121-151.

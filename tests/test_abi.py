@@ -8,6 +8,7 @@ import os
 import re
 
 import numpy as np
+import torch
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -159,3 +160,30 @@ def test_reference_shim_loads_and_checks_arguments(hm):
     packed = torch.zeros(4352, dtype=torch.uint8)
     with pytest.raises(RuntimeError, match="device uint8"):
         shim.w4a16_gemv_fused_packed(out, x, packed, 128, 64, -1, 0, 0)
+
+
+def test_find_nonfinite_host_known_answers(hm):
+    # The reference's own cases for find_nonfinite_bf16 (tests/ffn_deploy/contract_test.cpp:107-124): bf16 1.0 everywhere,
+    # one nonfinite value at an unsampled and at a sampled column, then a whole nonfinite row. Host scan, no GPU.
+    rows, cols = 4, 256
+    bits = np.full((rows, cols), 0x3F80, np.uint16)
+    t = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
+    assert hm.find_nonfinite(t(bits)) == -1 and hm.find_nonfinite(t(bits), sampled=True) == -1
+    for nonfinite in (0x7F80, 0xFF80, 0x7FC0, 0xFFFF):
+        bits[2, 3] = nonfinite
+        assert hm.find_nonfinite(t(bits)) == 2 * cols + 3
+        assert hm.find_nonfinite(t(bits), sampled=True) == -1
+        bits[2, 3] = 0x3F80
+        bits[3, 64] = nonfinite
+        assert hm.find_nonfinite(t(bits), sampled=True) == 3 * cols + 64
+        bits[3, 64] = 0x3F80
+    bits[1, :] = 0x7FC0
+    assert hm.find_nonfinite(t(bits)) == cols and hm.find_nonfinite(t(bits), sampled=True) == cols
+    # fp16: the exponent field is bits 10..14; the largest finite value and a subnormal are finite
+    h = np.full((2, 8), 0x3C00, np.uint16)
+    h[0, 1], h[0, 2] = 0x7BFF, 0x0001
+    f16 = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.float16)
+    assert hm.find_nonfinite(f16(h)) == -1
+    h[1, 5] = 0xFC00
+    assert hm.find_nonfinite(f16(h)) == 8 + 5
+    assert hm.kFiniteSampleStride == 64
