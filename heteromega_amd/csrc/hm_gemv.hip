@@ -168,6 +168,12 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     static_assert(RING == 0 || (MT == 1 && GPT < 4 && S * RING <= 8), "a chosen ring depth is for one row, groups of 64 or 128, at most 8 tiles");
     constexpr int CPG = G / 8;             // 8-element activation chunks per group
     constexpr int kPre = 4;                // chunks per thread fetched ahead of the weights
+    // Weight loads are non-temporal except in one-row plain launches with a ring of 4 steps (1025 to 2048 waves, the
+    // Llama-3-8B down GEMV's shape), where plain loads measured faster: the Llama-3-8B layer 20.7 -> 20.3 us in
+    // interleaved graphs on two boxes (a streaming probe of that shape: 5.9 against 6.9 us), while the same change in
+    // the ring-3 and ring-8 launches slowed the Qwen2.5-14B and Llama-3.2-1B layers by 1% and 3% (and 1792 waves of
+    // 32 KiB, the gate_up's shape, stream at 12.6 us plain against 11.3 us non-temporal).
+    constexpr bool kStreamNT = FUSED || MT > 1 || RING != 4;
 
     const int tid = threadIdx.x;
     const int wave = uniform(tid >> 6);
@@ -355,7 +361,8 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(qp[s] + i * 64 + lane));
+            const u32x4_t *src = reinterpret_cast<const u32x4_t *>(qp[s] + i * 64 + lane);
+            const u32x4_t v = kStreamNT ? __builtin_nontemporal_load(src) : *src;
             wq[u][s] = uint4{v.x, v.y, v.z, v.w};
         }
     };
@@ -1032,8 +1039,12 @@ GemvPlan plan_gemv(const GemvCall &c) {
                 }
             }
         }
-        if (best < 0.0) { // unreachable for m <= 16: one K tile per split always fits
-            set_splits(c.kt_count);
+        if (best < 0.0) {
+            // No candidate within the partial bound: a long K whose staged chunk needs more splits than the bound allows
+            // (K = 28672, N = 8192 at 12 or 16 rows). Take the fewest splits whose chunk fits LDS, one wave per strip
+            // group and four groups per workgroup; the partial buffer follows this plan (gemv_partial_bound).
+            const int64_t max_kt = std::max<int64_t>(1, static_cast<int64_t>(kLdsMax) / (rows_pad * 256));
+            set_splits((c.kt_count + max_kt - 1) / max_kt);
             p.wps = 1;
             p.nu = 4;
         }

@@ -85,3 +85,24 @@ def test_forward_equals_separate_calls(oracle, hm, device, m, hidden, inter, gro
         ref = ffn.down(ffn.gate_up(x))
         torch.cuda.synchronize()
         assert torch.equal(y, ref), (m, hidden, dtype, rep)
+
+
+@pytest.mark.parametrize("m", [12, 16])
+def test_multirow_long_k_split_fallback(oracle, hm, device, m):
+    # A long K at 12 or 16 rows (a Llama-3-70B down projection, K = 28672, N = 8192): the staged chunk needs at least
+    # six K splits, which the planner's bound on split partials does not allow. The plan takes the fewest splits that
+    # fit LDS (six), so the workspace stays a few MB (224 one-tile splits would need 84-112 MB of partials).
+    rng = np.random.default_rng(900 + m)
+    k, n, g, dtype = 28672, 8192, 128, "fp16"
+    w_np = oracle.random_weights(rng, k, n, g, dtype)
+    w = hm.RepackedMatrix.from_logical(*logical_to_device(w_np, dtype, device), g, dtype=TORCH[dtype])
+    ws = w.workspace_bytes(m)
+    print(f"workspace at M={m}: {ws} bytes")
+    assert ws <= 6 * m * n * 4 + (1 << 20)
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=TORCH[dtype], device=device)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    cols = np.r_[0:64, 4000:4064, n - 64:n]  # three strips' worth of columns, against float64 on those columns
+    wf = oracle.dequantize(w_np[0][:, cols], oracle.from_bits(w_np[1][:, cols], dtype), w_np[2][:, cols], g)
+    assert_close(oracle, host_f64(y)[:, cols], x64 @ wf, dtype, f"long K M={m}")
