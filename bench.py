@@ -4,10 +4,12 @@
 Headline `value`: Llama-3-8B FFN layer decode, M = 1, fp16 activations, W4A16 group 128,
 as algorithmic GB/s (weights + x + y per layer, inputs resident in HBM). A step is one FFN layer pass over one
 batch. Six independent weight sets (553 MB) rotate so the 256 MB Infinity Cache cannot serve the weights.
-The steps are captured in a HIP graph and replayed, so host launch overhead is not timed.
-Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), a 32-layer decode stack with
-RMSNorm and residual between layers, the Qwen2.5-14B g = 64 shape, a per-kernel roofline for the dominant kernel measured
-with HIP events, and the reference CPU path (restated AVX-512 GEMV) timed on this host's cores.
+The steps are captured in a HIP graph and replayed, so host launch overhead is not timed; extra.decode_M1_eager times
+the same layer called eagerly through the C ABI (and the reference-signature GpuFfnModel::forward) with host time
+per call. Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), a 32-layer decode stack with
+RMSNorm and residual between layers, the Qwen2.5-14B g = 64 shape, the roofline of the headline step's two kernels
+and of the prefill gate_up GEMM measured with HIP events, and the reference CPU path (restated AVX-512 GEMV) timed on
+this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 """
@@ -273,29 +275,96 @@ def prefill_gate_up_roofline(hm, torch, dev, layers, m, h, i, replays):
     achieved = flops / sec / 1e12
     return {"kernel": "gemm_kernel<F16, 128, true, 8, 2, 8, 2> (fused gate_up + SwiGLU, 128 x 256 tiles)", "bound": "mfma",
             "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-            "traffic": None, "avg_launch_us": round(sec * 1e6, 2), "algorithmic_flops_per_launch": int(flops), "rows": m}
+            "traffic": measured_traffic(PREFILL_TRAFFIC, "traffic_bytes_per_launch"), "avg_launch_us": round(sec * 1e6, 2),
+            "algorithmic_flops_per_launch": int(flops), "rows": m,
+            "timing": f"median of {replays} event-timed replays of a graph of two launches (two weight sets), after 0.5 s of untimed replays"}
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_gemv_gate_up_llama8b_decode_m1.md")
+def eager_bench(hm, torch, dev, layers, h, inter, calls=480):
+    """The headline layer called eagerly (no graph): hm_ffn_forward through ctypes with prepared arguments, over the
+    rotating weight sets. Returns (GPU us per layer from HIP events around the enqueues, host us per call)."""
+    from heteromega_amd import _lib
+    import ctypes
+
+    L = _lib.load()
+    x = torch.randn((1, h), device=dev).to(layers[0].dtype)
+    y = torch.empty_like(x)
+    ws = layers[0].workspace(1)
+    off = (-ws.data_ptr()) % 256  # the C ABI takes a 256-byte aligned workspace
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = [(Lr._h, ctypes.c_void_p(y.data_ptr()), h, ctypes.c_void_p(x.data_ptr()), h, 1, 0, inter, ctypes.c_void_p(ws.data_ptr() + off),
+             ws.numel() - off, stream) for Lr in layers]
+    fwd = L.hm_ffn_forward
+    for i in range(2 * len(args)):
+        assert fwd(*args[i % len(args)]) == 0
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = None
+    for _ in range(3):
+        e0.record()
+        t0 = time.perf_counter()
+        for i in range(calls):
+            fwd(*args[i % len(args)])
+        host = (time.perf_counter() - t0) / calls
+        e1.record()
+        torch.cuda.synchronize()
+        gpu = e0.elapsed_time(e1) / 1e3 / calls
+        if best is None or gpu < best[0]:
+            best = (gpu, host)
+    assert bool(torch.isfinite(y).all()), "eager decode output is not finite"
+    return best[0] * 1e6, best[1] * 1e6
 
 
-def measured_traffic():
-    """HBM bytes per launch of the fused gate_up GEMV (Llama-3-8B, M = 1), from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy kernel there), or None without one."""
+def shim_eager_host_us(hm, torch, dev, h, inter, calls=200):
+    """Host us per call of the reference-signature heteromega::GpuFfnModel::forward (bf16, M = 1) on one layer packed
+    from host tiles: the C++ operator surface a reference caller links, reached here through its pybind module."""
+    import numpy as np
+    from heteromega_amd import _reference_shim as shim
+
+    rng = np.random.default_rng(5)
+
+    def tiles(k, n):
+        q = rng.integers(0, 16, (k, n), dtype=np.uint8)
+        s = (rng.uniform(0.001, 0.02, (k // 128, n)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        z = rng.integers(0, 16, (k // 128, n), dtype=np.int8)
+        return torch.from_numpy(hm.pack_w4a16(q, s, z)).to(dev)
+
+    model = shim.GpuFfnModel()
+    model.add_layer(tiles(h, inter), tiles(h, inter), tiles(inter, h), h, inter)
+    x = torch.randn((1, h), device=dev).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    st = torch.cuda.current_stream().cuda_stream
+    for _ in range(10):
+        model.forward(0, x, y, st)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        model.forward(0, x, y, st)
+    host = (time.perf_counter() - t0) / calls
+    torch.cuda.synchronize()
+    return host * 1e6
+
+
+DECODE_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_gemv_gate_up_llama8b_decode_m1.md")
+PREFILL_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_gemm_gate_up_llama8b_prefill_m2048.md")
+
+
+def measured_traffic(path, key):
+    """HBM bytes of one launch (or step) from a committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated there
+    against a copy kernel of known size): the integer after `key:`, or None without one."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return int(line.split(":", 1)[1].strip())
     except (OSError, ValueError):
         pass
     return None
 
 
-def pmc_probe(hm, torch, dev, H, I, G, sets, rows=1):
-    """Eager launches for one rocprofv3 --pmc pass: a copy kernel of known size (calibration), then the fused
-    gate_up GEMV and the down GEMV of the headline workload (or of the same layer at `rows` rows), then the layer's
-    forward (whose one-row kernels are the pair-unit builds), on rotating weight sets."""
+def calibration_copy(torch, dev):
+    """A plain copy kernel of known size for the rocprofv3 --pmc passes: 8 launches that read and write 64 MiB each
+    (torch bitwise_not over int32, four buffers the Infinity Cache cannot hold)."""
     words = (64 << 20) // 4
     bufs = [torch.empty(words, dtype=torch.int32, device=dev).random_(0, 1 << 30) for _ in range(4)]
     outs = [torch.empty_like(b) for b in bufs]
@@ -304,7 +373,13 @@ def pmc_probe(hm, torch, dev, H, I, G, sets, rows=1):
         torch.bitwise_not(bufs[r % 4], out=outs[r % 4])
     torch.cuda.synchronize()
     log(f"pmc probe: 8 copy launches of {words * 4} bytes read + {words * 4} bytes written")
-    del bufs, outs
+
+
+def pmc_probe(hm, torch, dev, H, I, G, sets, rows=1):
+    """Eager launches for one rocprofv3 --pmc pass: a copy kernel of known size (calibration), then the fused
+    gate_up GEMV and the down GEMV of the headline workload (or of the same layer at `rows` rows), then the layer's
+    forward (whose one-row kernels are the pair-unit builds), on rotating weight sets."""
+    calibration_copy(torch, dev)
     layers = make_layers(hm, torch, dev, H, I, G, sets)
     x = torch.randn((rows, H), device=dev).to(torch.float16)
     act = torch.empty((rows, I), dtype=torch.float16, device=dev)
@@ -419,8 +494,9 @@ def main():
     ap.add_argument("--rows", type=int, default=1, help="rows (M) of the --pmc-probe GEMVs")
     ap.add_argument("--pmc-probe-prefill", action="store_true",
                     help="only launch the fused gate_up GEMM at M=2048 (for rocprofv3 --pmc passes)")
-    ap.add_argument("--profile", choices=("decode", "roofline"),
-                    help="only the headline decode steps, or only the gate_up roofline graphs (for rocprofv3 kernel traces)")
+    ap.add_argument("--profile", choices=("decode", "roofline_prefill", "gate_up"),
+                    help="only the headline decode steps (the decode roofline's measurement), only the prefill roofline's "
+                         "graphs, or only the graphs of the whole-pair gate_up GEMV alone (for rocprofv3 kernel traces)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -441,6 +517,7 @@ def main():
         pmc_probe(hm, torch, dev, H, I, G, args.sets, args.rows)
         return
     if args.pmc_probe_prefill:
+        calibration_copy(torch, dev)
         pl = make_layers(hm, torch, dev, H, I, G, 2)
         xp = torch.randn((2048, H), device=dev).to(torch.float16)
         ap_ = torch.empty((2048, I), dtype=torch.float16, device=dev)
@@ -453,19 +530,37 @@ def main():
     log("building weight sets ...")
     layers = make_layers(hm, torch, dev, H, I, G, args.sets)
 
+    if args.profile == "roofline_prefill":
+        rp = prefill_gate_up_roofline(hm, torch, dev, layers, 2048, H, I, 10)
+        print(json.dumps({"roofline_prefill": rp}), flush=True)
+        return
+
     # Headline: decode M = 1.
     nbytes = ffn_bytes(1, H, I, G)
-    if args.profile != "roofline":
+    if args.profile != "gate_up":
         sec, med, g1, keep = decode_bench(hm, torch, dev, layers, 1, H, args.steps, args.warmup, warm_seconds=2.0, blocks=40)
         value = nbytes / sec / 1e9
         log(f"decode M=1: {sec * 1e6:.2f} us/layer, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of HBM peak); "
             f"event median {med * 1e6:.2f} us/layer")
+        # Roofline of the step's kernels: the headline step is hm_ffn_forward at one row, two launches that both stream
+        # weights from HBM (the pair-unit gate_up + SwiGLU GEMV, then the down GEMV that forms the pairs two workgroups
+        # share); together they move the layer's algorithmic bytes. Timed with HIP events on the stream the graph
+        # replays on: the median over 40 replays of a graph of BLOCK back-to-back layer passes, per pass.
+        achieved = nbytes / med / 1e9
+        out["roofline"] = {
+            "kernel": "gemv_kernel<F16, 1, 128, 2, true, 1024, 4, 1> (gate_up + SwiGLU by pair units) + gemv_kernel<F16, 1, 128, 1, false, 512, 4, 2> "
+                      "(down, forming the split pairs): the two launches of one headline step (hm_ffn_forward, M=1)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(DECODE_TRAFFIC, "traffic_bytes_per_layer_forward"), "avg_launch_us": round(med * 1e6, 3),
+            "algorithmic_bytes_per_launch": nbytes,
+            "timing": f"per layer pass (both launches): median of 40 event-timed replays of a graph of {BLOCK} passes"}
         if args.profile == "decode":
-            print(json.dumps({"decode_us": round(sec * 1e6, 3), "decode_event_median_us": round(med * 1e6, 3)}), flush=True)
+            print(json.dumps({"decode_us": round(sec * 1e6, 3), "decode_event_median_us": round(med * 1e6, 3), "roofline": out["roofline"]}),
+                  flush=True)
             return
 
-    # Dominant kernel: the fused gate_up + SwiGLU GEMV, timed alone with HIP events on the stream its graph replays
-    # on: the median over replays of a graph of BLOCK launches on the rotating weight sets.
+    # The whole-pair fused gate_up GEMV alone (what hm_ffn_gate_up launches), with HIP events on the stream its graph
+    # replays on: the median over replays of a graph of BLOCK launches on the rotating weight sets.
     x1 = torch.randn((1, H), device=dev).to(torch.float16)
     acts = torch.empty((1, I), dtype=torch.float16, device=dev)
 
@@ -477,17 +572,22 @@ def main():
     time_graph(torch, g_gu, 1, 0.3, 2)
     gu_sec = event_time_graph(torch, g_gu, 40) / BLOCK
     gu_bytes = 2 * (H * I // 2 + (H * I // G) * 3) + H * 2 + I * 2
-    achieved = gu_bytes / gu_sec / 1e9
-    out["roofline"] = {"kernel": "gemv_kernel<F16, 1, 128, 2, true, 256, 4, 0> (fused gate_up + SwiGLU, M=1, ring of 4 steps, as hm_ffn_gate_up launches it)", "bound": "hbm",
-                       "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                       "traffic": measured_traffic(), "avg_launch_us": round(gu_sec * 1e6, 3), "algorithmic_bytes_per_launch": gu_bytes,
-                       "timing": f"median of 40 event-timed replays of a graph of {BLOCK} launches"}
-    log(f"gate_up kernel: {gu_sec * 1e6:.2f} us, {achieved:.1f} GB/s")
-    if args.profile == "roofline":
-        print(json.dumps({"roofline": out["roofline"]}), flush=True)
+    gu_alone = {"kernel": "gemv_kernel<F16, 1, 128, 2, true, 256, 4, 0> (hm_ffn_gate_up, whole pairs)", "avg_launch_us": round(gu_sec * 1e6, 3),
+                "GB_s": round(gu_bytes / gu_sec / 1e9, 1), "frac_hbm": round(gu_bytes / gu_sec / 1e9 / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(DECODE_TRAFFIC, "traffic_bytes_per_launch"), "algorithmic_bytes_per_launch": gu_bytes}
+    log(f"gate_up GEMV alone: {gu_sec * 1e6:.2f} us, {gu_bytes / gu_sec / 1e9:.1f} GB/s")
+    if args.profile == "gate_up":
+        print(json.dumps({"gate_up_gemv_alone": gu_alone}), flush=True)
         return
 
-    extra = {"decode_M1_event_median_us": round(med * 1e6, 3)}
+    extra = {"decode_M1_event_median_us": round(med * 1e6, 3), "gate_up_gemv_alone": gu_alone}
+    # The same layer called eagerly, one C call per layer (no graph), and the reference-signature operator's host cost.
+    eg, eh = eager_bench(hm, torch, dev, layers, H, I)
+    extra["decode_M1_eager"] = {"us_per_layer": round(eg, 2), "host_us_per_call": round(eh, 2), "graph_event_median_us": round(med * 1e6, 2),
+                                "path": "hm_ffn_forward via ctypes, one call per layer on the rotating sets, HIP events around the enqueues"}
+    if not args.quick:
+        extra["decode_M1_eager"]["shim_gpuffnmodel_forward_host_us_per_call"] = round(shim_eager_host_us(hm, torch, dev, H, I), 2)
+    log(f"eager decode M=1: {extra['decode_M1_eager']}")
     if not args.quick:
         for m in (4, 16):
             s, md, _, _ = decode_bench(hm, torch, dev, layers, m, H, args.steps, args.warmup, blocks=20)
