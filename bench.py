@@ -4,9 +4,10 @@
 Headline `value`: Llama-3-8B FFN layer decode, M = 1, fp16 activations, W4A16 group 128,
 as algorithmic GB/s (weights + x + y per layer, inputs resident in HBM). A step is one FFN layer pass over one
 batch. Six independent weight sets (553 MB) rotate so the 256 MB Infinity Cache cannot serve the weights.
-The steps are captured in a HIP graph and replayed, so host launch overhead is not timed; extra.decode_M1_eager times
-the same layer called eagerly through the C ABI (and the reference-signature GpuFfnModel::forward) with host time
-per call. Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), a 32-layer decode stack with
+The timed steps are eager C ABI calls (one hm_ffn_forward per step, as the reference's model loop calls its
+operators); the host enqueues faster than the GPU runs them. extra.decode_M1_event_median_us is the same pass in graphs
+of 48 timed with HIP events, and extra.decode_M1_eager adds the host time per call and the reference-signature
+GpuFfnModel::forward's. Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), a 32-layer decode stack with
 RMSNorm and residual between layers, the Qwen2.5-14B g = 64 shape, the roofline of the headline step's two kernels
 and of the prefill gate_up GEMM measured with HIP events, and the reference CPU path (restated AVX-512 GEMV) timed on
 this host's cores.
@@ -199,14 +200,40 @@ def event_time_graph(torch, g, replays):
 BLOCK = 48  # layer passes per event-timed block: a decoder replays a model's layers per token
 
 
+def forward_calls(layers, x, y, ws, stream):
+    """One prepared hm_ffn_forward call per weight set (ctypes, all arguments converted once), as a C++ caller of the
+    C ABI makes them: the layer's whole channel range, x and y rows of the layer's width."""
+    import ctypes
+
+    from heteromega_amd import _lib
+
+    fwd = _lib.load().hm_ffn_forward
+    off = (-ws.data_ptr()) % 256  # the C ABI takes a 256-byte aligned workspace
+    m, h = x.shape
+    calls = []
+    for L in layers:
+        a = (L._h, ctypes.c_void_p(y.data_ptr()), y.stride(0), ctypes.c_void_p(x.data_ptr()), x.stride(0), m, 0, L.inter,
+             ctypes.c_void_p(ws.data_ptr() + off), ws.numel() - off, ctypes.c_void_p(stream))
+        calls.append(a)
+
+    def run(count):
+        for i in range(count):
+            rc = fwd(*calls[i % len(calls)])
+            if rc != 0:
+                raise RuntimeError(_lib.last_error())
+    return run
+
+
 def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0, blocks=0):
     """Seconds per decode step (one FFN layer pass), cycling through the weight sets.
 
-    The timed region is exactly `steps` passes: one HIP graph of `steps` passes, replayed once, wall-clocked with
-    a synchronize on both sides (after `warmup` untimed passes, warm_seconds of untimed replays and one untimed
-    replay of the timed graph itself). With blocks > 0
-    also the median per pass over `blocks` event-timed replays of a graph of BLOCK passes (BASELINE's method: HIP
-    events, median). Returns (wall seconds per step, median seconds per step or None, graph of BLOCK passes, buffers)."""
+    The timed region is exactly `steps` passes enqueued as eager C ABI calls (hm_ffn_forward, one call per step as the
+    reference's model loop calls its operators), wall-clocked with a synchronize on both sides, after `warmup` untimed
+    passes, warm_seconds of untimed graph replays (the clock settles) and one untimed run of the same `steps` passes.
+    Eager enqueueing (6 us of host time per call) stays ahead of the GPU (20 us per pass), and its fixed cost per timed
+    region is below a graph replay's (at 20 steps 20.9 against 21.3 us per pass; equal at 240). With blocks > 0 also
+    the median per pass over `blocks` event-timed replays of a graph of BLOCK passes (BASELINE's method: HIP events,
+    median). Returns (wall seconds per step, median seconds per step or None, graph of BLOCK passes, buffers)."""
     x = torch.randn((m, h), device=dev).to(layers[0].dtype)
     y = torch.empty_like(x)
     ws = layers[0].workspace(m)
@@ -219,20 +246,17 @@ def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0, 
         return fn
 
     g_block = graph_of(torch, run(BLOCK))
-    g_timed = graph_of(torch, run(steps))
-    if warmup > 0:
-        graph_of(torch, run(warmup)).replay()
+    eager = forward_calls(layers, x, y, ws, torch.cuda.current_stream().cuda_stream)
+    eager(warmup)
     torch.cuda.synchronize()
     t_end = time.perf_counter() + warm_seconds
     while time.perf_counter() < t_end:
         g_block.replay()
         torch.cuda.synchronize()
-    # The timed graph's own first replay carries one-time costs (measured: a 20-pass graph's first replay runs
-    # 0.5-6 us per pass slower than its later ones); it runs untimed, so the timed replay is a steady one.
-    g_timed.replay()
+    eager(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    g_timed.replay()
+    eager(steps)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
     median = event_time_graph(torch, g_block, blocks) / BLOCK if blocks > 0 else None
@@ -695,8 +719,8 @@ def main():
         "config": {"workload": "Llama-3-8B SwiGLU FFN layer decode, M=1, H=4096, I=14336, W4A16 group 128, fp16 activations",
                    "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4), "weight_sets_rotated": args.sets,
                    "bytes_per_step": nbytes,
-                   "timing": "the timed steps as one HIP graph replay of exactly `steps` layer passes (after an untimed replay "
-                             "of the same graph), wall clock with synchronize on both sides; the event median over blocks of 48 "
+                   "timing": "exactly `steps` layer passes enqueued as eager C ABI calls (hm_ffn_forward), wall clock with "
+                             "synchronize on both sides, after untimed warm-up passes; the event median over graphs of 48 "
                              "passes is in extra"},
         "roofline": out["roofline"],
         "roofline_prefill": out.get("roofline_prefill"),
