@@ -3,7 +3,8 @@
 
 Headline `value`: Llama-3-8B FFN layer decode, M = 1, fp16 activations, W4A16 group 128,
 as algorithmic GB/s (weights + x + y per layer, inputs resident in HBM). A step is one FFN layer pass over one
-batch. Six independent weight sets (553 MB) rotate so the 256 MB Infinity Cache cannot serve the weights.
+batch. 32 independent weight sets rotate (2.95 GB, the FFN layers of one Llama-3-8B), so neither a layer nor the 32
+matrices of any one projection fit in the 256 MB Infinity Cache.
 The timed steps are eager C ABI calls (one hm_ffn_forward per step, as the reference's model loop calls its
 operators); the host enqueues faster than the GPU runs them. extra.decode_M1_event_median_us is the same pass in graphs
 of 48 timed with HIP events, and extra.decode_M1_eager adds the host time per call and the reference-signature
@@ -512,7 +513,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--quick", action="store_true", help="headline decode only")
-    ap.add_argument("--sets", type=int, default=6, help="weight sets rotated per decode step")
+    ap.add_argument("--sets", type=int, default=32, help="weight sets rotated per decode step (32: one Llama-3-8B's FFN layers)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the calibration copy and the headline GEMVs (for rocprofv3 --pmc passes)")
     ap.add_argument("--rows", type=int, default=1, help="rows (M) of the --pmc-probe GEMVs")
@@ -683,7 +684,7 @@ def main():
 
         # Qwen2.5-14B FFN shape, group 64.
         qh, qi, qg = 5120, 13824, 64
-        ql = make_layers(hm, torch, dev, qh, qi, qg, 4, seed=2)
+        ql = make_layers(hm, torch, dev, qh, qi, qg, 8, seed=2)
         s, _, _, _ = decode_bench(hm, torch, dev, ql, 1, qh, args.steps, args.warmup)
         b = ffn_bytes(1, qh, qi, qg)
         extra["qwen14b_g64_decode_M1"] = {"us_per_layer": round(s * 1e6, 2), "GB_s": round(b / s / 1e9, 1), "frac_hbm": round(b / s / 1e9 / HBM_PEAK_GBS, 4)}

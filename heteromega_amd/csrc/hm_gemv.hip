@@ -168,12 +168,10 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     static_assert(RING == 0 || (MT == 1 && GPT < 4 && S * RING <= 8), "a chosen ring depth is for one row, groups of 64 or 128, at most 8 tiles");
     constexpr int CPG = G / 8;             // 8-element activation chunks per group
     constexpr int kPre = 4;                // chunks per thread fetched ahead of the weights
-    // Weight loads are non-temporal except in one-row plain launches with a ring of 4 steps (1025 to 2048 waves, the
-    // Llama-3-8B down GEMV's shape), where plain loads measured faster: the Llama-3-8B layer 20.7 -> 20.3 us in
-    // interleaved graphs on two boxes (a streaming probe of that shape: 5.9 against 6.9 us), while the same change in
-    // the ring-3 and ring-8 launches slowed the Qwen2.5-14B and Llama-3.2-1B layers by 1% and 3% (and 1792 waves of
-    // 32 KiB, the gate_up's shape, stream at 12.6 us plain against 11.3 us non-temporal).
-    constexpr bool kStreamNT = FUSED || MT > 1 || RING != 4;
+    // Weight loads are non-temporal. Plain loads in the Llama-3-8B down GEMV (ring of 4) look 0.5 us faster per layer
+    // when six layers rotate, but only because the six down matrices (184 MB) then stay in the 256 MB Infinity Cache:
+    // with 12 or 32 layers rotating, as in a whole model, the layer is 0.3-0.5 us faster with non-temporal loads
+    // (21.25 against 20.78 us at 12, 21.27 against 21.02 at 32).
 
     const int tid = threadIdx.x;
     const int wave = uniform(tid >> 6);
@@ -362,7 +360,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const u32x4_t *src = reinterpret_cast<const u32x4_t *>(qp[s] + i * 64 + lane);
-            const u32x4_t v = kStreamNT ? __builtin_nontemporal_load(src) : *src;
+            const u32x4_t v = __builtin_nontemporal_load(src);
             wq[u][s] = uint4{v.x, v.y, v.z, v.w};
         }
     };
