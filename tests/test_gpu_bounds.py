@@ -102,9 +102,10 @@ def test_k_split_pair_accumulate_writes_only_its_block(oracle, hm, device, m):
     assert_close(oracle, host_f64(y), ref, dtype, f"framed k-split m={m}")
 
 
-@pytest.mark.parametrize("m", [1, 3, 37, 333])
-def test_ffn_writes_only_its_block(oracle, hm, device, m):
-    dtype, hidden, inter, group = "bf16", 2048, 2816, 128
+# (1000, 3584): the fused gate_up GEMM runs 8 row tiles of 128, the last one ragged.
+@pytest.mark.parametrize("m,inter", [(1, 2816), (3, 2816), (37, 2816), (333, 2816), (1000, 3584)])
+def test_ffn_writes_only_its_block(oracle, hm, device, m, inter):
+    dtype, hidden, group = "bf16", 2048, 128
     rng = np.random.default_rng(7)
     ws_ = [oracle.random_weights(rng, hidden, inter, group, dtype), oracle.random_weights(rng, hidden, inter, group, dtype),
            oracle.random_weights(rng, inter, hidden, group, dtype)]

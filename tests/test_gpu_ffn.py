@@ -49,7 +49,7 @@ def test_ffn_decode_llama3_8b(oracle, hm, device, dtype, m):
     assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, dtype), dtype, f"Llama-3-8B FFN decode M={m}")
 
 
-@pytest.mark.parametrize("dtype,m,rows", [("fp16", 512, None), ("fp16", 2048, 96), ("bf16", 512, 96), ("fp16", 37, None)])
+@pytest.mark.parametrize("dtype,m,rows", [("fp16", 512, None), ("fp16", 2048, 96), ("bf16", 512, 96), ("fp16", 37, None), ("fp16", 460, None)])
 def test_ffn_prefill_llama3_8b(oracle, hm, device, dtype, m, rows):
     layer, _, wf = _layer(oracle, hm, device, 4096, 14336, 128, dtype, 1)
     rng = np.random.default_rng(20 + m)
