@@ -41,6 +41,7 @@
 #include "hm_internal.hpp"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdlib>
 
@@ -774,51 +775,74 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 }
 
 // Adds the split partials [splits][m][ncols]; fused: ncols alternate gate and up per 16 columns and the
-// output is SiLU(gate) * up per channel (ncols / 2 channels).
+// output is SiLU(gate) * up per channel (ncols / 2 channels). Four consecutive outputs per thread, so every split
+// is read with 16-byte loads (ncols is a multiple of 16, and four consecutive channels of a fused call lie in one
+// group of 16 gate and 16 up columns).
 template <class T, bool FUSED>
 __global__ void __launch_bounds__(256) sum_splits(const float *__restrict__ partial, uint16_t *__restrict__ y, int64_t ldy, int m,
                                                   int ncols, int splits, bool accumulate, bool pairwise) {
-    const int nout = FUSED ? ncols / 2 : ncols;
+    const int quads = (FUSED ? ncols / 2 : ncols) / 4;
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= static_cast<int64_t>(m) * nout) {
+    if (idx >= static_cast<int64_t>(m) * quads) {
         return;
     }
-    const int row = static_cast<int>(idx / nout);
-    const int c = static_cast<int>(idx - static_cast<int64_t>(row) * nout);
-    const int cg = FUSED ? (c >> 4) * 32 + (c & 15) : c; // gate (or plain) column
+    const int row = static_cast<int>(idx / quads);
+    const int c = 4 * static_cast<int>(idx - static_cast<int64_t>(row) * quads);
+    const int cg = FUSED ? (c >> 4) * 32 + (c & 15) : c; // gate (or plain) column of output c
+    const float4 *pr = reinterpret_cast<const float4 *>(partial + static_cast<int64_t>(row) * ncols + cg);
+    const int64_t split4 = static_cast<int64_t>(m) * ncols / 4; // float4s per split
+    uint16_t *yr = y + row * ldy + c;
+    auto lanes = [](const float4 &v) { return std::array<float, 4>{v.x, v.y, v.z, v.w}; };
     if (!FUSED && pairwise) {
         // A K-split pair: each share's sum is rounded, then they are added with one more rounding, as
         // round(round(x0 W0) + round(x1 W1)) (plain outputs only).
-        float v = T::to_float(T::from_float(partial[static_cast<int64_t>(row) * ncols + cg]));
-        for (int s = 1; s < splits; ++s) {
-            v = T::to_float(T::from_float(v + T::to_float(T::from_float(partial[(static_cast<int64_t>(s) * m + row) * ncols + cg]))));
+        std::array<float, 4> v = lanes(pr[0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = T::to_float(T::from_float(v[i]));
         }
-        y[row * ldy + c] = T::from_float(v);
+        for (int s = 1; s < splits; ++s) {
+            const std::array<float, 4> p = lanes(pr[s * split4]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = T::to_float(T::from_float(v[i] + T::to_float(T::from_float(p[i]))));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            yr[i] = T::from_float(v[i]);
+        }
         return;
     }
     // Eight splits' loads are in flight at once (a load per split and a wait per add would put the splits'
     // memory latencies in series); the sums still run in split order.
     constexpr int kBatch = 8;
-    float g = 0.0f, u = 0.0f;
+    std::array<float, 4> g{0.0f, 0.0f, 0.0f, 0.0f}, u{0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < splits; s0 += kBatch) {
-        float gv[kBatch], uv[kBatch];
+        float4 gv[kBatch], uv[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             const int s = min(s0 + j, splits - 1); // past the last split: re-read it, not added
-            const float *pr = partial + (static_cast<int64_t>(s) * m + row) * ncols + cg;
-            gv[j] = pr[0];
-            uv[j] = FUSED ? pr[16] : 0.0f;
+            gv[j] = pr[s * split4];
+            uv[j] = FUSED ? pr[s * split4 + 4] : float4{};
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             if (s0 + j < splits) {
-                g += gv[j];
-                u += uv[j];
+                const std::array<float, 4> a = lanes(gv[j]), b = lanes(uv[j]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    g[i] += a[i];
+                    u[i] += b[i];
+                }
             }
         }
     }
-    const uint16_t out = T::from_float(FUSED ? silu(g) * u : g);
-    y[row * ldy + c] = accumulate ? T::from_float(T::to_float(y[row * ldy + c]) + T::to_float(out)) : out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint16_t out = T::from_float(FUSED ? silu(g[i]) * u[i] : g[i]);
+        yr[i] = accumulate ? T::from_float(T::to_float(yr[i]) + T::to_float(out)) : out;
+    }
 }
 
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING, int PAIRS>
@@ -1162,7 +1186,7 @@ hipError_t launch_gemv_pair(const GemvCall &c0, const GemvCall &c1, int64_t k0, 
 
 hipError_t launch_sum_splits(const float *partial, uint16_t *y, int64_t ldy, int64_t m, int ncols, int splits, bool fused,
                              int dtype, hipStream_t stream, bool accumulate, bool pairwise) {
-    const int64_t total = m * (fused ? ncols / 2 : ncols);
+    const int64_t total = m * (fused ? ncols / 2 : ncols) / 4; // four outputs per thread
     const dim3 blocks(static_cast<unsigned>((total + 255) / 256));
     const int mi = static_cast<int>(m);
     if (dtype == 1) {

@@ -131,7 +131,7 @@ struct GemmCall {
 // Tile configuration (2: 128 x 256 tiles, 8 waves; 1: 128 x 128, 4 waves; 0: 64 x 128, 4 waves). The GEMM splits
 // K only for grids of under 128 workgroups and 4-wave grids of under 512, with fp32 partials of at most
 // kGemmPartialMax bytes.
-constexpr size_t kGemmPartialMax = 16u << 20;
+constexpr size_t kGemmPartialMax = 32u << 20;
 struct GemmPlan {
     int cfg = 1;
     int64_t tiles_m = 0, tiles_n = 0;

@@ -615,8 +615,9 @@ def ffn_partitioned(layer, x, partition, stream=None):
 def ffn_row_split(layer, x, y, other_rows, stream=None):
     """Row (M) split of hetero_compute.cpp:189-259: the GPU takes rows [0, M - other_rows), the other device
     the tail; here both run on the GPU. Rows are independent: the result has the unsplit FFN's bits when no
-    part's GEMM splits its K range (small grids split: under 128 workgroups, or 4-wave grids under 512; e.g. a
-    Llama-3-8B or Qwen2.5-14B part of 1024 rows and more does not), and equals it within rounding otherwise."""
+    part's GEMM splits its K range (small grids split: under 128 workgroups, 4-wave grids under 512, and long-K
+    down projections whose 128 x 256 grid is under 128 workgroups; e.g. a Llama-3-8B part of 1152 rows or more,
+    or a Qwen2.5-14B part of 1024 or more, does not), and equals it within rounding otherwise."""
     m = x.size(0)
     if not 0 <= other_rows <= m:
         raise ValueError("row split outside [0, M]")

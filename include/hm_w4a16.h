@@ -247,7 +247,7 @@ hm_status hm_ffn_destroy(hm_ffn *f);
 /* Workspace for hm_ffn_forward with up to max_m rows (the SwiGLU activation
  * [max_m, I], the one-row gate_up's fp32 sums of strip pairs that two of its
  * workgroups share (about 3.2 I bytes), and split-K partials: the decode GEMV's for
- * up to 16 rows, and 16 MiB from 17 rows, the most a small GEMM grid's K split
+ * up to 16 rows, and 32 MiB from 17 rows, the most a small GEMM grid's K split
  * writes). Nothing in it has to start at zero. Replaces GpuFfnBuffers
  * (gpu_ffn.hpp:172-180). */
 size_t hm_ffn_workspace_bytes(const hm_ffn *f, int64_t max_m);

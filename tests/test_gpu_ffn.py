@@ -59,11 +59,15 @@ def test_ffn_prefill_llama3_8b(oracle, hm, device, dtype, m, rows):
     sel = np.arange(m) if rows is None else np.sort(rng.choice(m, rows, replace=False))
     assert_close(oracle, host_f64(y)[sel], _ffn_ref(oracle, x64[sel], wf, dtype), dtype, f"Llama-3-8B FFN prefill M={m}")
     # rows are independent: a row block alone gives the same bits where neither call splits K (M = 2048 and its
-    # 1024-row block), and equal within rounding where one does (M = 512: both down GEMMs split, differently)
+    # 1536-row block), and equal within rounding where one does (M = 512: both down GEMMs split, differently; a
+    # 1024-row block: its down GEMM splits K in two)
     if m == 2048:
+        y_part = layer.forward(x[256:1792].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(y_part, y[256:1792])
         y_part = layer.forward(x[512:1536].contiguous())
         torch.cuda.synchronize()
-        assert torch.equal(y_part, y[512:1536])
+        assert_close(oracle, host_f64(y_part), host_f64(y[512:1536]), dtype, "row block M=1024")
     elif m >= 512:
         y_part = layer.forward(x[128:384].contiguous())
         torch.cuda.synchronize()
@@ -138,7 +142,7 @@ def test_partition_row_split_is_exact(oracle, hm, device):
     _, x = make_x(oracle, rng, 2048, 5120, "fp16", device)
     full = layer.forward(x)
     y = torch.empty_like(full)
-    hm.ffn_row_split(layer, x, y, 512)  # GPU rows [0, 1536), the other share [1536, 2048)
+    hm.ffn_row_split(layer, x, y, 1024)  # GPU rows [0, 1024), the other share [1024, 2048)
     torch.cuda.synchronize()
     assert torch.equal(y, full)
     full = layer.forward(x[:1024])

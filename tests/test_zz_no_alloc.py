@@ -53,7 +53,7 @@ def test_static_scratch_forward_equals_workspace_forward(oracle, hm, device, sha
 def test_static_scratch_rejects_large_requests(oracle, hm, device):
     layer = _layer(oracle, hm, device, 1024, 2048, 128, "fp16", 4)
     lib = hm._lib.load()
-    m = 64  # prefill rows reserve the GEMM's split partials (16 MiB): more than the static scratch
+    m = 64  # prefill rows reserve the GEMM's split partials (32 MiB): more than the static scratch
     assert lib.hm_ffn_workspace_bytes(layer._h, m) > SCRATCH_BYTES
     x = torch.zeros((m, 1024), dtype=torch.float16, device=device)
     y = torch.zeros((m, 1024), dtype=torch.float16, device=device)
