@@ -49,7 +49,8 @@ def test_ffn_decode_llama3_8b(oracle, hm, device, dtype, m):
     assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, dtype), dtype, f"Llama-3-8B FFN decode M={m}")
 
 
-@pytest.mark.parametrize("dtype,m,rows", [("fp16", 512, None), ("fp16", 2048, 96), ("bf16", 512, 96), ("fp16", 37, None), ("fp16", 460, None)])
+@pytest.mark.parametrize("dtype,m,rows", [("fp16", 512, None), ("fp16", 2048, None), ("bf16", 512, None), ("bf16", 2048, None),
+                                          ("fp16", 37, None), ("fp16", 460, None)])
 def test_ffn_prefill_llama3_8b(oracle, hm, device, dtype, m, rows):
     layer, _, wf = _layer(oracle, hm, device, 4096, 14336, 128, dtype, 1)
     rng = np.random.default_rng(20 + m)
@@ -102,11 +103,13 @@ def test_ffn_qwen14b_group64(oracle, hm, device):
         y = layer.forward(x)
         torch.cuda.synchronize()
         assert_close(oracle, host_f64(y), _ffn_ref(oracle, x64, wf, "fp16"), "fp16", f"Qwen2.5-14B FFN g=64 decode M={m}")
-    x64, x = make_x(oracle, rng, 1024, 5120, "fp16", device)
-    y = layer.forward(x)
-    torch.cuda.synchronize()
-    sel = np.sort(rng.choice(1024, 64, replace=False))
-    assert_close(oracle, host_f64(y)[sel], _ffn_ref(oracle, x64[sel], wf, "fp16"), "fp16", "Qwen2.5-14B FFN g=64 prefill M=1024")
+    # prefill: M = 1024 (no K split), M = 512 (the down GEMM's 128 x 256 tiles split K in three)
+    for m, rows in ((1024, 1024), (512, 512)):
+        x64, x = make_x(oracle, rng, m, 5120, "fp16", device)
+        y = layer.forward(x)
+        torch.cuda.synchronize()
+        sel = np.sort(rng.choice(m, rows, replace=False))
+        assert_close(oracle, host_f64(y)[sel], _ffn_ref(oracle, x64[sel], wf, "fp16"), "fp16", f"Qwen2.5-14B FFN g=64 prefill M={m}")
 
 
 @pytest.mark.parametrize("m", [1, 1024])
