@@ -1126,12 +1126,19 @@ hm_status hm_ffn_block_forward(const hm_ffn *f, void *x, int64_t ldx, const void
         // Two launches: the gate_up GEMV stages RMSNorm(x) * weight, the down GEMV adds its output into x.
         return one_row_ffn(f, x, ldx, x, ldx, 0, f->inter, norm_weight, eps, true, ffn_ws, ffn_bytes, s);
     }
-    // Several rows: RMSNorm, the FFN, the residual add (the same results as the two-launch path per row).
+    // Several rows: RMSNorm, the gate_up projection, then the down projection adding its rounded output into x
+    // (x = round(x + round(act W)), in its epilogue or in the split sum: the bits of hm_ffn_forward followed by
+    // hm_residual_add2, one launch fewer).
+    (void)y;
+    const size_t act_bytes = static_cast<size_t>(round_up(M * f->inter * 2, 256));
+    void *act = ffn_ws;
+    void *rest = static_cast<uint8_t *>(ffn_ws) + act_bytes;
+    const size_t rest_bytes = ffn_bytes - act_bytes;
     if ((st = hm_rmsnorm(normed, f->hidden, x, ldx, norm_weight, M, f->hidden, eps, dtype, stream)) != HM_OK ||
-        (st = hm_ffn_forward(f, y, f->hidden, normed, f->hidden, M, 0, f->inter, ffn_ws, ffn_bytes, stream)) != HM_OK) {
+        (st = hm_ffn_gate_up(f, act, f->inter, normed, f->hidden, M, 0, f->inter, rest, rest_bytes, stream)) != HM_OK) {
         return st;
     }
-    return hm_residual_add2(x, ldx, y, f->hidden, nullptr, 0, M, f->hidden, dtype, stream);
+    return run_linear(f->down.p, x, ldx, act, f->inter, M, 0, f->hidden, 0, f->inter / 128, false, rest, rest_bytes, s, true);
 }
 
 hm_status hm_silu_mul(const void *gate_up, int64_t ld_in, void *act, int64_t ld_out, int64_t rows, int64_t n, int32_t layout, hm_dtype dtype,

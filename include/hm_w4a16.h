@@ -283,8 +283,9 @@ size_t hm_ffn_block_workspace_bytes(const hm_ffn *f, int64_t max_m);
  * hm_rmsnorm. This is the model's FFN block with the layer-boundary norm and residual add
  * (src/unified_llm_w4a16_hetero/unified_llm_w4a16.cpp:2867-2892 with kernels/gpu/src/residual_norm.cu:25-98).
  * One row (H <= 8192) runs as two launches: the gate_up GEMV normalizes x while staging it and the down GEMV
- * adds its rounded output into x. Other M run hm_rmsnorm, hm_ffn_forward and hm_residual_add2. Either way the
- * result equals those three calls bit for bit. Needs hm_ffn_block_workspace_bytes(f, M) bytes of workspace. */
+ * adds its rounded output into x. Other M run hm_rmsnorm, the gate_up projection and a down projection that adds
+ * its rounded output into x (x = round(x + round(act Wd))). Either way the result equals hm_rmsnorm, hm_ffn_forward
+ * and hm_residual_add2 bit for bit. Needs hm_ffn_block_workspace_bytes(f, M) bytes of workspace. */
 hm_status hm_ffn_block_forward(const hm_ffn *f, void *x, int64_t ldx, const void *norm_weight, float eps, int64_t M,
                                void *workspace, size_t workspace_bytes, void *stream);
 

@@ -318,12 +318,13 @@ def test_ffn_stack_decode_small(oracle, hm, device):
         ref = host_f64(x)  # re-anchor each step so rounding flips do not compound
 
 
-@pytest.mark.parametrize("m", [1, 4, 37])
+@pytest.mark.parametrize("m", [1, 4, 16, 37, 300, 2048])
 @pytest.mark.parametrize("dtype,hidden,inter,group", [("fp16", 4096, 14336, 128), ("bf16", 4096, 14336, 128), ("fp16", 5120, 13824, 64)])
 def test_block_forward_equals_separate_ops(oracle, hm, device, dtype, hidden, inter, group, m):
     # x += FFN(RMSNorm(x) * w) in place. One row: the gate_up GEMV normalizes x while staging it and the down GEMV
-    # adds its rounded output into x (two launches); other M run the separate kernels. Either way the bits equal
-    # rmsnorm, forward and residual_add2 in sequence (the layer boundary of residual_norm.cu:25-98).
+    # adds its rounded output into x (two launches); other M: RMSNorm, gate_up, and a down projection that adds its
+    # rounded output into x in its epilogue (M = 2048) or in the split sum (M = 4, 16, 37, 300). Either way the bits
+    # equal rmsnorm, forward and residual_add2 in sequence (the layer boundary of residual_norm.cu:25-98).
     layer, _, wf = _layer(oracle, hm, device, hidden, inter, group, dtype, 5)
     rng = np.random.default_rng(110 + m)
     x64, x = make_x(oracle, rng, m, hidden, dtype, device)
