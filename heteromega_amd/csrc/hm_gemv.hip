@@ -44,6 +44,7 @@
 #include <array>
 #include <cmath>
 #include <cstdlib>
+#include <unordered_map>
 
 namespace hm {
 namespace {
@@ -977,9 +978,10 @@ hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, int spw, dim3 
 
 } // namespace
 
-GemvPlan plan_gemv(const GemvCall &c) {
+namespace {
+
+GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
     GemvPlan p;
-    const int64_t cus = device_topology().cus;
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
     p.spw = c.fused ? 2 : (c.m > 1 && strips % 2 == 0 ? 2 : 1);
     p.groups = strips / p.spw;
@@ -1117,6 +1119,50 @@ GemvPlan plan_gemv(const GemvCall &c) {
         p.lds += static_cast<size_t>(32 * (p.kt_per_split * 8 / c.pair_units + 1));
     }
     p.partial_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * c.m * strips * 16 * sizeof(float) : 0;
+    return p;
+}
+
+// The plan's inputs: the call's rows, columns, K tiles, fusion, group, pair spill and pair units, and the device's
+// CU count.
+struct PlanKey {
+    int64_t m, n, kt_count, cus;
+    int32_t group, pair_units;
+    bool fused, spill;
+    bool operator==(const PlanKey &o) const {
+        return m == o.m && n == o.n && kt_count == o.kt_count && cus == o.cus && group == o.group && pair_units == o.pair_units &&
+               fused == o.fused && spill == o.spill;
+    }
+};
+struct PlanKeyHash {
+    size_t operator()(const PlanKey &k) const {
+        uint64_t h = 1469598103934665603ull;
+        for (const uint64_t v : {static_cast<uint64_t>(k.m), static_cast<uint64_t>(k.n), static_cast<uint64_t>(k.kt_count),
+                                 static_cast<uint64_t>(k.cus), static_cast<uint64_t>(k.group), static_cast<uint64_t>(k.pair_units),
+                                 static_cast<uint64_t>(k.fused) | (static_cast<uint64_t>(k.spill) << 1)}) {
+            h = (h ^ v) * 1099511628211ull;
+        }
+        return static_cast<size_t>(h);
+    }
+};
+
+} // namespace
+
+// Plans are cached per host thread (the several-row planner weighs up to a few hundred launch shapes, 1-3 us on the
+// host, and each call plans twice), so repeated eager calls of one shape plan once.
+GemvPlan plan_gemv(const GemvCall &c) {
+    const int64_t cus = device_topology().cus;
+    const PlanKey key{c.m, c.n, c.kt_count, cus, static_cast<int32_t>(c.w.group), static_cast<int32_t>(c.pair_units), c.fused,
+                      c.pair_spill != nullptr};
+    thread_local std::unordered_map<PlanKey, GemvPlan, PlanKeyHash> cache;
+    const auto it = cache.find(key);
+    if (it != cache.end()) {
+        return it->second;
+    }
+    if (cache.size() >= 4096) {
+        cache.clear();
+    }
+    const GemvPlan p = plan_gemv_uncached(c, cus);
+    cache.emplace(key, p);
     return p;
 }
 
