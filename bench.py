@@ -8,7 +8,8 @@ matrices of any one projection fit in the 256 MB Infinity Cache.
 The timed steps are eager C ABI calls (one hm_ffn_forward per step, as the reference's model loop calls its
 operators); the host enqueues faster than the GPU runs them. extra.decode_M1_event_median_us is the same pass in graphs
 of 48 timed with HIP events, and extra.decode_M1_eager adds the host time per call and the reference-signature
-GpuFfnModel::forward's. Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s), a 32-layer decode stack with
+GpuFfnModel::forward's. Also reported: decode M = 4 and 16, prefill M = 512 and 2048 (TFLOP/s; 8 weight sets rotate, 738 MB),
+a 32-layer decode stack with
 RMSNorm and residual between layers, the Qwen2.5-14B g = 64 shape, the roofline of the headline step's two kernels
 and of the prefill gate_up GEMM measured with HIP events, and the reference CPU path (restated AVX-512 GEMV) timed on
 this host's cores.
@@ -27,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 MFMA
+PREFILL_SETS = 8                # weight sets a prefill graph rotates: 8 Llama-3-8B layers are 738 MB, their gate_up 470 MB
 
 
 def log(*a):
@@ -79,7 +81,7 @@ def qkv_bench(hm, torch, dev, h, g, sets=24):
     torch.cuda.synchronize()
     n_all = sum(widths)
     out = {}
-    for m, count in ((1, sets), (2048, 2)):
+    for m, count in ((1, sets), (2048, sets)):
         x = torch.randn((m, h), device=dev).to(torch.float16)
         y = torch.empty((m, n_all), device=dev, dtype=torch.float16)
         ws = torch.empty(max(parts[0][0].workspace_bytes(m), fused[0].workspace_bytes(m)) + 512, dtype=torch.uint8, device=dev)
@@ -125,7 +127,7 @@ def ksplit_bench(hm, torch, dev, h, inter, g, sets=12):
     whole = [mat(inter) for _ in range(sets)]
     torch.cuda.synchronize()
     out = {}
-    for m, count in ((1, sets), (2048, 2)):
+    for m, count in ((1, sets), (2048, min(sets, PREFILL_SETS))):
         act = torch.randn((m, inter), device=dev).to(torch.float16)
         y = torch.empty((m, h), device=dev, dtype=torch.float16)
         ws = torch.empty(max(whole[0].workspace_bytes(m), 64 << 20) + 512, dtype=torch.uint8, device=dev)
@@ -266,43 +268,46 @@ def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0, 
 
 
 def prefill_bench(hm, torch, dev, layers, m, h, steps, warmup):
-    """Seconds per prefill layer: replays of a graph of two layers (two weight sets), after half a second of untimed
-    replays (the part's clock settles under sustained MFMA load); the median of event-timed replays."""
+    """Seconds per prefill layer: replays of a graph of one layer pass on each of PREFILL_SETS weight sets (so the
+    256 MB Infinity Cache cannot hold the weights between passes), after half a second of untimed replays (the
+    part's clock settles under sustained MFMA load); the median of event-timed replays."""
     x = torch.randn((m, h), device=dev).to(layers[0].dtype)
     y = torch.empty_like(x)
     ws = layers[0].workspace(m)
+    sets = layers[:PREFILL_SETS]
 
     def run():
-        for L in layers[:2]:
+        for L in sets:
             L.forward(x, y, workspace=ws)
 
     g = graph_of(torch, run)
     time_graph(torch, g, 1, 0.5, max(1, warmup // 2))
     sec = event_time_graph(torch, g, max(3, steps // 2))
     assert bool(torch.isfinite(y).all()), "prefill output is not finite"
-    return sec / 2
+    return sec / len(sets)
 
 
 def prefill_gate_up_roofline(hm, torch, dev, layers, m, h, i, replays):
-    """The fused gate_up GEMM (SwiGLU epilogue) at m rows: median event time per launch over graphs of launches on
-    two weight sets, against the dense fp16 MFMA peak."""
+    """The fused gate_up GEMM (SwiGLU epilogue) at m rows: median event time per launch over graphs of one launch on
+    each of PREFILL_SETS weight sets, against the dense fp16 MFMA peak."""
     x = torch.randn((m, h), device=dev).to(layers[0].dtype)
     act = torch.empty((m, i), dtype=layers[0].dtype, device=dev)
+    sets = layers[:PREFILL_SETS]
 
     def run():
-        for L in layers[:2]:
+        for L in sets:
             L.gate_up(x, act)
 
     g = graph_of(torch, run)
     time_graph(torch, g, 1, 0.5, 2)
-    sec = event_time_graph(torch, g, replays) / 2
+    sec = event_time_graph(torch, g, replays) / len(sets)
     flops = 2.0 * m * h * 2 * i
     achieved = flops / sec / 1e12
     return {"kernel": "gemm_kernel<F16, 128, true, 8, 2, 8, 2> (fused gate_up + SwiGLU, 128 x 256 tiles)", "bound": "mfma",
             "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
             "traffic": measured_traffic(PREFILL_TRAFFIC, "traffic_bytes_per_launch"), "avg_launch_us": round(sec * 1e6, 2),
             "algorithmic_flops_per_launch": int(flops), "rows": m,
-            "timing": f"median of {replays} event-timed replays of a graph of two launches (two weight sets), after 0.5 s of untimed replays"}
+            "timing": f"median of {replays} event-timed replays of a graph of {len(sets)} launches ({len(sets)} weight sets), after 0.5 s of untimed replays"}
 
 
 def eager_bench(hm, torch, dev, layers, h, inter, calls=480):
@@ -673,11 +678,11 @@ def main():
         torch.cuda.empty_cache()
 
         # Attention Q/K/V projections through the same operator (Llama-3-8B: 4096 -> 4096 + 1024 + 1024): three
-        # launches against one launch on the concatenated matrix. 24 weight sets (300 MB) rotate at M = 1.
+        # launches against one launch on the concatenated matrix. 24 weight sets (300 MB) rotate at M = 1 and 2048.
         extra["attention_qkv"] = qkv_bench(hm, torch, dev, H, G)
         log(f"attention QKV: {extra['attention_qkv']}")
         # The down projection kept as a pre-saved K-split pair (split at I / 2, both shares on the GPU) against
-        # one matrix. 12 weight sets of each (700 MB) rotate at M = 1.
+        # one matrix. 12 weight sets of each (700 MB) rotate at M = 1, 8 (470 MB) at M = 2048.
         extra["down_k_split_pair"] = ksplit_bench(hm, torch, dev, H, I, G)
         torch.cuda.empty_cache()
         log(f"down projection as a K-split pair: {extra['down_k_split_pair']}")
