@@ -12,13 +12,14 @@
 // operand feeds RBW MFMAs (8 at BM = 128: about two VALU instructions per MFMA). The activation tile (BM x 128
 // per K tile) goes from memory straight into LDS (buffer_load ... lds, no registers) and serves all WN waves;
 // its 16-byte chunks are XOR-swizzled by row so that an MFMA operand read touches 16 distinct bank groups; one
-// barrier per K tile.
+// barrier per K tile (per two K tiles for the 128 x 256 tiles).
 //
 // Software pipeline: while the MFMAs of 32-K step mu run, the VALU builds the B operands of step mu + 1 (of the
 // next K tile at mu = 3) and the LDS delivers the activation fragments of step mu + 1; sched_group_barrier
-// interleaves one MFMA with two VALU instructions. K tile kt + DEPTH - 1's weights and activations are requested
-// at the start of K tile kt (DEPTH 2, or 4 for the 64-row tiles, whose small grids expose each workgroup's own
-// latency).
+// interleaves one MFMA with two VALU instructions. K tile kt + LOOK's weights and activations are requested at the
+// start of K tile kt: LOOK = 1 (two buffers) for the 128 x 128 tiles, 3 (four buffers) for the 64-row tiles, whose
+// small grids expose each workgroup's own latency, and 2 (four buffers, one barrier per two K tiles) for the
+// 128 x 256 tiles.
 //
 // Tiles are dealt to XCDs in contiguous runs (workgroup i runs on XCD i % 8 on an MI355X) of an order that walks bands of 4
 // row tiles column by column, so the workgroups resident on one XCD share both activation rows and weight
@@ -36,6 +37,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace hm {
 namespace {
@@ -134,7 +136,7 @@ template <class T, int G, int NSW> struct BTile {
     uint32_t r[NSW][128 / G]; // scale/zero records of its groups
 };
 
-template <class T, int G, bool FUSED, int RBW, int NSW, int WN, int DEPTH>
+template <class T, int G, bool FUSED, int RBW, int NSW, int WN, int DEPTH, int KPB = 1>
 __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2))) gemm_kernel(GemmArgs a) {
     constexpr int WGS = WN * 64;
     constexpr int BM = RBW * 16;
@@ -147,8 +149,13 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     // and its activations in one of DEPTH LDS buffers. Per K tile a wave issues NB weight/record loads and ADMA
     // activation transfers, in that order; all of them count in vmcnt, in order.
     static_assert(DEPTH == 2 || DEPTH == 4, "pipeline depth");
+    // KPB = 2: one barrier per two K tiles. Four LDS buffers, K tiles requested two ahead; the barrier after each odd
+    // K tile waits for everything in flight (the next two tiles), and the buffer an iteration fills two tiles ahead was
+    // last read before the previous barrier.
+    static_assert(KPB == 1 || (KPB == 2 && DEPTH == 4), "two K tiles per barrier: four buffers");
+    constexpr int LOOK = KPB == 2 ? 2 : DEPTH - 1; // K tiles requested ahead of the one being multiplied
     constexpr int NB = 2 * NSW;
-    constexpr int AHEAD = (DEPTH - 2) * (NB + ADMA); // loads issued after tile kt + 1's activations at iteration kt
+    constexpr int AHEAD = KPB == 2 ? 0 : (DEPTH - 2) * (NB + ADMA); // loads issued after tile kt + 1's activations at iteration kt
     // Activation tile of one K tile: BM rows of 128 halves (256 B), 16-byte chunks XOR-swizzled by row
     // (chunk c of row r at slot c ^ (r % 16)), so the 16 rows one MFMA operand read touches fall on distinct banks.
     // Two separate arrays (not one [2][...]) so that the compiler can tell the buffers apart and does not
@@ -294,8 +301,9 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     // tile DEPTH - 1 ahead goes into slot `lb` (that of K tile kt - 1, whose registers and LDS buffer were last
     // read before the previous barrier).
     auto iteration = [&](int kt, int buf, int nb, const BTile<T, G, NSW> &cur, const BTile<T, G, NSW> &nxt, BTile<T, G, NSW> &ld, int lb,
-                         Deq<T> (&dq)[NSW], BOps &op, AFr &fa) __attribute__((always_inline)) {
-        const int ktn = min(kt + DEPTH - 1, nkt - 1); // the last iterations re-request the last tile; nothing reads it
+                         Deq<T> (&dq)[NSW], BOps &op, AFr &fa, auto odd) __attribute__((always_inline)) {
+        constexpr bool kOdd = decltype(odd)::value; // KPB = 2: kt is odd (a barrier follows)
+        const int ktn = min(kt + LOOK, nkt - 1); // the last iterations re-request the last tile; nothing reads it
         load_b(ktn, ld);
         load_a(ktn, lb);
 #pragma unroll
@@ -306,7 +314,13 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
                 read_a(buf, mu + 1, fn);
                 dequant_step(cur, dq, mu + 1, on);
             } else {
-                wait_vmcnt<ADMA + AHEAD>(); // nxt's weights (the transfers issued after them may still run)
+                if constexpr (KPB == 2) {
+                    // nxt's weights: at an odd kt they were requested one iteration ago, before nxt's and this
+                    // iteration's transfers; at an even kt the barrier before this iteration already waited for them.
+                    wait_vmcnt<kOdd ? 2 * ADMA + NB : ADMA + NB>();
+                } else {
+                    wait_vmcnt<ADMA + AHEAD>(); // nxt's weights (the transfers issued after them may still run)
+                }
                 dequant_step(nxt, dq, 0, on);
             }
             // strip-major: the operand of the last strip, finished at the end of the previous step, is needed last
@@ -329,37 +343,55 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
             }
         }
         // The next tile's activations: this wave's transfers done, then everyone's.
-        wait_vmcnt<AHEAD>();
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if constexpr (KPB == 1 || kOdd) {
+            wait_vmcnt<AHEAD>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
         read_a(nb, 0, fa);
     };
 
     BTile<T, G, NSW> b[DEPTH];
 #pragma unroll
-    for (int t = 0; t + 1 < DEPTH; ++t) {
+    for (int t = 0; t < LOOK; ++t) {
         load_b(min(t, nkt - 1), b[t]);
         load_a(min(t, nkt - 1), t);
     }
     Deq<T> dq[NSW];
     BOps op;
     AFr fa;
-    wait_vmcnt<ADMA + AHEAD>();
+    if constexpr (KPB == 2) {
+        wait_vmcnt<2 * ADMA + NB>(); // tile 0's weights (tile 0's transfers and tile 1's loads may still run)
+    } else {
+        wait_vmcnt<ADMA + AHEAD>();
+    }
     dequant_step(b[0], dq, 0, op);
     wait_vmcnt<AHEAD>();
     asm volatile("s_barrier" ::: "memory");
     read_a(0, 0, fa);
     // DEPTH K tiles per trip, so the register sets and LDS buffers rotate without copies.
+    auto one = [&](int k, auto u) __attribute__((always_inline)) {
+        constexpr int U = decltype(u)::value;
+        using Parity = std::integral_constant<bool, U % 2 == 1>;
+        iteration(k, U, (U + 1) % DEPTH, b[U], b[(U + 1) % DEPTH], b[(U + LOOK) % DEPTH], (U + LOOK) % DEPTH, dq, op, fa, Parity{});
+    };
     int kt = 0;
     for (; kt + DEPTH - 1 < nkt; kt += DEPTH) {
-#pragma unroll
-        for (int u = 0; u < DEPTH; ++u) {
-            iteration(kt + u, u, (u + 1) % DEPTH, b[u], b[(u + 1) % DEPTH], b[(u + DEPTH - 1) % DEPTH], (u + DEPTH - 1) % DEPTH, dq, op, fa);
+        one(kt, std::integral_constant<int, 0>{});
+        one(kt + 1, std::integral_constant<int, 1>{});
+        if constexpr (DEPTH == 4) {
+            one(kt + 2, std::integral_constant<int, 2>{});
+            one(kt + 3, std::integral_constant<int, 3>{});
         }
     }
-#pragma unroll
-    for (int u = 0; u + 1 < DEPTH; ++u) {
-        if (kt + u < nkt) {
-            iteration(kt + u, u, (u + 1) % DEPTH, b[u], b[(u + 1) % DEPTH], b[(u + DEPTH - 1) % DEPTH], (u + DEPTH - 1) % DEPTH, dq, op, fa);
+    if (kt < nkt) {
+        one(kt, std::integral_constant<int, 0>{});
+    }
+    if constexpr (DEPTH == 4) {
+        if (kt + 1 < nkt) {
+            one(kt + 1, std::integral_constant<int, 1>{});
+        }
+        if (kt + 2 < nkt) {
+            one(kt + 2, std::integral_constant<int, 2>{});
         }
     }
 
@@ -417,11 +449,12 @@ __global__ void __launch_bounds__(WN * 64) __attribute__((amdgpu_waves_per_eu(2)
     }
 }
 
-template <class T, int G, int RBW, int NSW, int WN, int DEPTH> hipError_t launch_cfg(const GemmArgs &a, bool fused, dim3 grid, hipStream_t s) {
+template <class T, int G, int RBW, int NSW, int WN, int DEPTH, int KPB = 1>
+hipError_t launch_cfg(const GemmArgs &a, bool fused, dim3 grid, hipStream_t s) {
     if (fused) {
-        hipLaunchKernelGGL((gemm_kernel<T, G, true, RBW, NSW, WN, DEPTH>), grid, dim3(WN * 64), 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel<T, G, true, RBW, NSW, WN, DEPTH, KPB>), grid, dim3(WN * 64), 0, s, a);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<T, G, false, RBW, NSW, WN, DEPTH>), grid, dim3(WN * 64), 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel<T, G, false, RBW, NSW, WN, DEPTH, KPB>), grid, dim3(WN * 64), 0, s, a);
     }
     return hipGetLastError();
 }
@@ -429,7 +462,10 @@ template <class T, int G, int RBW, int NSW, int WN, int DEPTH> hipError_t launch
 template <class T, int G> hipError_t launch_g(const GemmArgs &a, bool fused, int cfg, dim3 grid, hipStream_t s) {
     switch (cfg) {
     case 2:
-        return launch_cfg<T, G, 8, 2, 8, 2>(a, fused, grid, s); // 128 x 256, 8 waves of 128 x 32, 1 K tile ahead
+        // 128 x 256, 8 waves of 128 x 32, 2 K tiles ahead in 4 buffers, one barrier per 2 K tiles (against one per K
+        // tile, the same bits: Llama-3-8B M = 2048 gate_up 398.0 -> 392.9 us, down 193.9 -> 192.1, M = 512 down 67.9 ->
+        // 66.1; Qwen2.5-14B layer at M = 1024 426.7 -> 416.4)
+        return launch_cfg<T, G, 8, 2, 8, 4, 2>(a, fused, grid, s);
     case 1:
         return launch_cfg<T, G, 8, 2, 4, 2>(a, fused, grid, s); // 128 x 128, 4 waves of 128 x 32, 1 K tile ahead
     default:
@@ -494,7 +530,7 @@ GemmPlan plan_gemm(const GemmCall &c) {
     // its call splits (grids that do not split keep them).
     const int64_t wgs = p.tiles_m * p.tiles_n;
     const bool small = wgs < cus / 2;
-    const int64_t aim = small ? cus : (p.cfg != 2 && wgs < 2 * cus ? 2 * cus : 0);
+    const int64_t aim = small ? cus : ((p.cfg == 0 || p.cfg == 1) && wgs < 2 * cus ? 2 * cus : 0);
     if (aim > 0 && c.kt_count >= 16) {
         int64_t splits = std::min<int64_t>((aim + wgs - 1) / wgs, c.kt_count / (small ? 8 : 24));
         while (splits > 1 && static_cast<size_t>(splits) * c.m * cols * sizeof(float) > kGemmPartialMax) {
