@@ -19,7 +19,7 @@
 // the whole launch: more than that only lengthens the memory queues and the launch's tail (measured on the
 // Llama-3-8B, Qwen2.5-14B and Llama-3.2-1B projections: down at 2048 waves 7.3 us with 4 steps against 7.6
 // with 8, at 2560 waves 9.8 us with 3 against 11.2 with 8, and at 1024 waves 4.6 us with 8 against 4.8
-// with 4).
+// with 4). Two to four rows keep 4 steps.
 //
 // Math per strip tile (4 MFMA steps of 32 K): the B operand is bias + q straight from the nibbles
 // (hm_device.hpp), A is the activation rows from LDS. One row:
@@ -28,8 +28,11 @@
 // and per group, with scale s and zero z of the column, sum_k x_k (q_k - z) s = s (P - Xb - z X), X = sum_k x_k.
 // Xb and X per group are computed when the wave stages x. This is the reference's per-tile factorization
 // s (sum q x - z sum x) (kernels/gpu/src/gemv_w4a16.cu:91-98, src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:242-253),
-// applied to MFMA partial sums. Several rows: each 32-K step runs a second MFMA of the same A fragment against
-// the constant operand -(bias + z) (the fp16 odd pairs take bias 64, so x needs no scaling), so the chain holds
+// applied to MFMA partial sums. Two to four rows take the same math: A row r is x row r / 4, so lane group h of the
+// MFMA output holds row h and folds it as one row does (the fp16 odd pairs' operand takes bias 64 so that the rows
+// go to LDS unscaled, by DMA, and the group sums are made from LDS). Several rows: each 32-K step runs a second
+// MFMA of the same A fragment against the constant operand -(bias + z) (the fp16 odd pairs take bias 64, so x
+// needs no scaling), so the chain holds
 // P = sum_k x_k (q_k - z) exactly in its products and the fold is one FMA s P per row: no per-group activation
 // sums, and x goes to LDS as it is, by DMA. The MFMA pipe has the room (it is idle most of the time in a
 // decode GEMV); the VALU has not. One LDS read of an A fragment feeds the MFMAs of all S strips.
@@ -146,28 +149,37 @@ template <class T> __device__ __forceinline__ uint4 zero_operand(uint32_t r) {
     }
 }
 
+// MT: rows the instantiation serves. 1: one row. kFewRows (2..4 rows): the one-row math and streaming with lane
+// group h of the MFMA carrying row h (A row r reads x row r / 4, so D rows 4 h .. 4 h + 3 are all row h and each
+// lane folds its element 0 as at one row: no more fold work per step than one row). 16: several rows (up to 16).
+//
 // Dynamic LDS. One row: xs [kc + 8] 16-bit, sums [kc / G + 1] float2 (Xb, X), the RMSNorm's four partial sums,
 // red [waves][S][16] float, then (pair_units > 0) the formed columns of the split's split pairs, 16 per pair in
-// pair order. Several rows: per K tile of the split a block of rows_pad = 4 ceil(m / 4) rows of 256 bytes, the
+// pair order. Few rows: xs [m][xst] with xst = kc rounded up to 512 + 8, sums [m][kc / G + 1], 16 bytes, red
+// [waves][S][m][16]. Several rows: per K tile of the split a block of rows_pad = 4 ceil(m / 4) rows of 256 bytes, the
 // 16-byte chunk c of row r at slot c ^ (r % 16) (rows past m hold row m - 1), and after the multiply, over its
 // front, red [wps - 1][nu][S][4][64 lanes] float: the sums of each strip group's waves past the first.
-// RING: ring depth in steps for one row (MT == 1, group >= 64), at most 8 tiles; the other instantiations
+// RING: ring depth in steps for one or few rows (group >= 64), at most 8 tiles; the other instantiations
 // size their ring themselves and take RING = 0. PAIRS (one row): kUnitsOut, the fused launch by units (a.units
 // waves per workgroup of WGS = 1024); kUnitsIn, the plain launch whose x holds such a launch's split pairs.
 constexpr int kUnitsOut = 1, kUnitsIn = 2;
+constexpr int kFewRows = 4;
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING, int PAIRS = 0>
 __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) gemv_kernel(GemvArgs a) {
+    static_assert(MT == 1 || MT == kFewRows || MT == 16, "row modes");
     static_assert(PAIRS == 0 || (MT == 1 && (PAIRS == kUnitsOut ? FUSED && WGS == 1024 : !FUSED && S == 1)), "pair modes");
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int ROWS = MT == 1 ? 1 : 4; // D elements per lane that can hold a real row
+    constexpr bool ONE = MT <= kFewRows;  // the one-row math (one or few rows)
+    constexpr bool FEW = MT == kFewRows;
+    constexpr int ROWS = ONE ? 1 : 4; // D elements per lane that can hold a real row
     constexpr int GPT = 128 / G;           // groups per strip tile
     constexpr int SPG = 4 / GPT;           // MFMA steps per group
     // Ring depth in steps: 8 tiles in flight per wave, fewer where the records (group < 128) and the
     // four-row folds (M > 1) need the registers.
-    constexpr int kInFlight = (MT > 1 && (S == 1 || GPT > 1)) ? 4 : 8; // strip tiles
+    constexpr int kInFlight = (!ONE && (S == 1 || GPT > 1)) ? 4 : 8; // strip tiles
     constexpr int KB_SIZED = kInFlight / S / (GPT == 4 ? 2 : 1) > 0 ? kInFlight / S / (GPT == 4 ? 2 : 1) : 1;
     constexpr int KB = RING > 0 ? RING : KB_SIZED;
-    static_assert(RING == 0 || (MT == 1 && GPT < 4 && S * RING <= 8), "a chosen ring depth is for one row, groups of 64 or 128, at most 8 tiles");
+    static_assert(RING == 0 || (ONE && GPT < 4 && S * RING <= 8), "a chosen ring depth is for one or few rows, groups of 64 or 128, at most 8 tiles");
     constexpr int CPG = G / 8;             // 8-element activation chunks per group
     constexpr int kPre = 4;                // chunks per thread fetched ahead of the weights
     // Weight loads are non-temporal. Plain loads in the Llama-3-8B down GEMV (ring of 4) look 0.5 us faster per layer
@@ -178,7 +190,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int tid = threadIdx.x;
     const int wave = uniform(tid >> 6);
     const int lane = tid & 63;
-    const int m = MT == 1 ? 1 : a.m; // the one-row instantiation is launched for m = 1 only
+    const int m = MT == 1 ? 1 : a.m; // the one-row instantiation is launched for m = 1 only, the few-row one for 2..4
     const int col = lane & 15;
     const int h = lane >> 4;
 
@@ -190,19 +202,22 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int kg = kc / G;    // groups of this split
     const int64_t xk0 = second ? static_cast<int64_t>(a.k0) : static_cast<int64_t>(kt0 - a.kt_begin) * 128;
 
-    // One row: x padded by 16 bytes and the group sums by 8 (the layout the fold reads).
-    const int xst = kc + 8;
+    // One row: x padded by 16 bytes and the group sums by 8 (the layout the fold reads). Few rows: each row's x
+    // rounded up to whole 1 KiB transfers (512 K) and padded by 16 bytes, so the four rows one MFMA operand read
+    // touches fall on different banks; its group sums likewise one row after another.
+    const int xst = FEW ? ((kc + 511) & ~511) + 8 : kc + 8;
     const int sst = kg + 1;
+    const int xrows = FEW ? m : 1;
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
-    float2 *sums = reinterpret_cast<float2 *>(smem + xst * 2);
-    const int norm_off = (xst * 2 + sst * static_cast<int>(sizeof(float2)) + 15) & ~15; // 4 floats past the staging
+    float2 *sums = reinterpret_cast<float2 *>(smem + xrows * xst * 2);
+    const int norm_off = (xrows * (xst * 2 + sst * static_cast<int>(sizeof(float2))) + 15) & ~15; // 4 floats past the staging
     // Several rows: bytes per K tile of the staged chunk.
     const int rows_pad = (m + 3) & ~3;
     const int tstride = rows_pad * 256;
     // One row: the cross-wave sums get their own space past the norm's partials, so a wave that has finished its
     // multiply writes them while others still read the staging (no barrier before the writes). Several rows:
     // they reuse the staging space, which the 144 KiB chunk leaves no room beside.
-    float *red = reinterpret_cast<float *>(smem + (MT == 1 ? norm_off + 16 : 0));
+    float *red = reinterpret_cast<float *>(smem + (ONE ? norm_off + 16 : 0));
 
     // This wave's strip group and its contiguous run [tb, te) of the split's tiles. Groups past the end of
     // the call (a partial last workgroup) read the last group and are not stored. Units (one row, fused): the
@@ -300,6 +315,20 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
                 }
             }
         }
+    } else if constexpr (FEW) {
+        // Few rows: each row's chunks of the wave's range go memory to LDS without registers, in whole 1 KiB
+        // transfers of 64 chunks aligned to the split's chunk 0 (chunks past the range hold the same x as any wave
+        // staging them writes; past the split's last row the buffer reads zeros). The group sums follow from LDS.
+        const uint32_t ldx2 = static_cast<uint32_t>(a.ldx) * 2u;
+        const __amdgpu_buffer_rsrc_t xr =
+            buffer_rsrc(a.x + xk0, static_cast<uint32_t>(m - 1) * ldx2 + static_cast<uint32_t>(kc) * 2u);
+        const int blo = st_lo >> 6, bhi = (st_hi + 63) >> 6;
+        for (int r = 0; r < m; ++r) {
+            for (int b = blo; b < bhi; ++b) {
+                const uint32_t voff = static_cast<uint32_t>(r) * ldx2 + static_cast<uint32_t>(64 * b + lane) * 16u;
+                lds_dma16(xr, reinterpret_cast<uint8_t *>(xs + r * xst + 512 * b), voff, 0u);
+            }
+        }
     } else {
         // Transfer p (1 KiB): K tile p / (rows_pad / 4), rows 4 (p % (rows_pad / 4)) + h; lane l fills slot l % 16
         // of its row with chunk (l % 16) ^ row. Rows past m read row m - 1.
@@ -372,9 +401,12 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     }
     __builtin_amdgcn_sched_barrier(0);
     advance();
-    if constexpr (MT > 1) {
+    if constexpr (FEW) {
         // This wave's transfers are in LDS once at most the ring's loads are outstanding (vmcnt counts in issue
-        // order); the barrier then covers every wave's transfers.
+        // order); the wave reads only rows it transferred itself.
+        wait_vmcnt<KB * S + (KB / RB) * S>();
+    } else if constexpr (!ONE) {
+        // As above; the barrier then covers every wave's transfers.
         wait_vmcnt<KB * S + (KB / RB) * S>();
         lds_barrier();
     }
@@ -414,8 +446,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     }
 
     // 1. One row: stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes
-    //    take consecutive 8-element chunks, so one group is G / 8 consecutive lanes.
-    auto stage = [&](int c8, uint4 v, uint4 g, bool valid) {
+    //    take consecutive 8-element chunks, so one group is G / 8 consecutive lanes. Few rows: x is in LDS as it is
+    //    (the fp16 odd pairs' operand takes bias 64 instead, rows_operand), only row `row`'s group sums are made.
+    auto stage = [&](int row, int c8, uint4 v, uint4 g, bool valid) {
         float sa = 0.0f, sb = 0.0f;
         if (norm) { // v <- round(v * scale * g) element-wise, as the RMSNorm kernel stores it
             uint32_t vw[4] = {v.x, v.y, v.z, v.w};
@@ -447,20 +480,22 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
                     }
                 }
             }
-            if constexpr (T::kWide) {
-                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-                const h2 sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-                v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
-                v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
+            if constexpr (!FEW) {
+                if constexpr (T::kWide) {
+                    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                    const h2 sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+                    v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
+                    v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
+                }
+                *reinterpret_cast<uint4 *>(xs + c8 * 8) = v;
             }
-            *reinterpret_cast<uint4 *>(xs + c8 * 8) = v;
         }
         // Sum over the CPG consecutive lanes of a group with DPP (no LDS crossbar): pairs, quads, eights, sixteens.
         sa = group_sum<CPG>(sa);
         sb = group_sum<CPG>(sb);
         if (valid && (c8 % CPG) == 0) {
             const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
-            sums[c8 / CPG] = make_float2(xb, sa + sb);
+            sums[row * sst + c8 / CPG] = make_float2(xb, sa + sb);
         }
     };
     // x's chunk c8 of the split, or its formed chunk when it belongs to a split pair. pr / pu as the high word of
@@ -495,17 +530,26 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            stage(pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]); // all lanes take part in the shuffles
+            stage(0, pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]); // all lanes take part in the shuffles
         }
         for (int base = kPre * 64; st_lo + base < st_hi; base += kPre * 64) {
             positions(base);
             fetch(); // long ranges only: these chunks wait behind the first ring steps
 #pragma unroll
             for (int c = 0; c < kPre; ++c) {
-                stage(pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]);
+                stage(0, pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]);
             }
         }
         // The wave reads only what it wrote; LDS operations of one wave complete in order.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else if constexpr (FEW) {
+        for (int r = 0; r < m; ++r) {
+            for (int c8 = st_lo + lane; c8 - lane < st_hi; c8 += 64) {
+                const bool valid = c8 < st_hi;
+                const uint4 v = *reinterpret_cast<const uint4 *>(xs + r * xst + min(c8, st_hi - 1) * 8);
+                stage(r, c8, v, uint4{}, valid); // all lanes take part in the shuffles
+            }
+        }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
@@ -519,8 +563,10 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             acc[s][e] = 0.0f;
         }
     }
-    // One row: the lane's K offset in the staged row.
-    const uint16_t *xa = xs + 8 * h;
+    // One row: the lane's K offset in the staged row. Few rows: in row col / 4 (A rows 4 h .. 4 h + 3 are row h), and
+    // the group sums of the lane's D row h; lane groups past the last row repeat it and are not stored.
+    const uint16_t *xa = xs + (FEW ? min(col >> 2, m - 1) * xst : 0) + 8 * h;
+    const float2 *srow = sums + (FEW ? min(h, m - 1) * sst : 0);
     // Several rows: the A-operand row of this lane (rows past rows_pad read the last staged row; they only feed
     // D rows >= m, which are never stored) and its slot offsets per 32-K step; the magic of the fp16 odd pairs.
     const int arow = min(col, rows_pad - 1);
@@ -546,10 +592,10 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
 #pragma unroll
         for (int g = 0; g < GPT; ++g) {
-            xg[g] = sums[ic * GPT + g];
+            xg[g] = srow[ic * GPT + g];
         }
     };
-    if constexpr (MT == 1) {
+    if constexpr (ONE) {
         read_x(tb);
     }
     // One row, one step: the S tiles of local tile i (unclamped: tiles past the wave's run are weighted by zero).
@@ -585,7 +631,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
                 if (mu % SPG == 0) {
                     p[s] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 }
-                p[s] = T::mfma16(av[mu], magic_operand<T>(word, magic), p[s]);
+                p[s] = T::mfma16(av[mu], (FEW ? rows_operand<T>(word, magic, odd_magic) : magic_operand<T>(word, magic)), p[s]);
             }
             if (mu % SPG == SPG - 1) {
                 const int g = mu / SPG;
@@ -646,12 +692,12 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     // One row: the same round count for every wave of the workgroup, the steps past a wave's run dropped by a
     // select. Several rows: the wave's own count, so every step of a full round is live, and the last round
     // skips its dead steps by a (wave-uniform) branch.
-    const int rounds = MT == 1 ? (tpw + KB - 1) / KB : max(1, (te - tb + KB - 1) / KB);
+    const int rounds = ONE ? (tpw + KB - 1) / KB : max(1, (te - tb + KB - 1) / KB);
     for (int r = 0; r + 1 < rounds; ++r) {
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
             const int i = tb + r * KB + u;
-            if constexpr (MT == 1) {
+            if constexpr (ONE) {
                 step(u, i);
             } else {
                 step_rows(u, i);
@@ -663,7 +709,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
         const int i = tb + (rounds - 1) * KB + u;
-        if constexpr (MT == 1) {
+        if constexpr (ONE) {
             step(u, i);
         } else if (i < te) {
             step_rows(u, i);
@@ -671,7 +717,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     }
 
     // 3. Add the waves of each strip group, then write.
-    if constexpr (MT > 1) {
+    if constexpr (!ONE) {
         // Several rows: the group's first wave (K range 0) writes the outputs straight from its accumulators
         // (lane: column col, rows 4 h + e), after adding those of the group's other waves in order of their K
         // ranges, which they leave in LDS lane by lane; a group of one wave needs neither LDS nor a barrier.
@@ -763,7 +809,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     for (int s = 0; s < S; ++s) {
 #pragma unroll
         for (int e = 0; e < ROWS; ++e) {
-            const int row = 4 * h + e;
+            const int row = FEW ? h : 4 * h + e; // one row: lanes 0..15; few rows: lane group h holds row h
             if (row < m) {
                 red[((wave * S + s) * m + row) * 16 + col] = acc[s][e];
             }
@@ -898,7 +944,10 @@ hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s, uns
 // block: threads per workgroup, WGS or (units) fewer.
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int PAIRS = 0>
 hipError_t launch_r(const GemvArgs &a, dim3 grid, int ring, size_t lds, hipStream_t s, unsigned block = WGS) {
-    if constexpr (MT == 1 && G != 32) {
+    if constexpr (MT == kFewRows && G != 32) {
+        (void)ring;
+        return launch_w<T, MT, G, S, FUSED, WGS, 4, PAIRS>(a, grid, lds, s, block); // 4 steps in flight
+    } else if constexpr (MT == 1 && G != 32) {
         // Strip pairs stop at 4 steps (8 tiles): measured slower with 8 (Llama-3.2-1B gate_up at 512 waves:
         // 7.2 us against 6.6).
         constexpr int deep = S == 2 ? 4 : 8;
@@ -971,9 +1020,13 @@ hipError_t launch_m(const GemvArgs &a, int group, bool fused, int spw, dim3 grid
 }
 
 template <class T>
-hipError_t launch_dtype(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
-    return a.m <= 1 ? launch_m<T, 1>(a, group, fused, spw, grid, waves, ring, lds, s)
-                    : launch_m<T, 16>(a, group, fused, spw, grid, waves, ring, lds, s);
+hipError_t launch_dtype(const GemvArgs &a, bool few, int group, bool fused, int spw, dim3 grid, int waves, int ring, size_t lds,
+                        hipStream_t s) {
+    if (a.m <= 1) {
+        return launch_m<T, 1>(a, group, fused, spw, grid, waves, ring, lds, s);
+    }
+    return few ? launch_m<T, kFewRows>(a, group, fused, spw, grid, waves, ring, lds, s)
+               : launch_m<T, 16>(a, group, fused, spw, grid, waves, ring, lds, s);
 }
 
 } // namespace
@@ -983,14 +1036,21 @@ namespace {
 GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
     GemvPlan p;
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
-    p.spw = c.fused ? 2 : (c.m > 1 && strips % 2 == 0 ? 2 : 1);
+    // Few rows (2..4, no RMSNorm staging): the one-row launch shape and math, the rows staged one after another
+    // (kFewRows). Against the several-row kernels, Llama-3-8B layer at M = 2 / 3 / 4: 24.1 / 24.5 / 25.0 -> 21.5 / 22.6 /
+    // 23.3 us, Llama-3.2-1B 14.4 / 14.3 / 14.7 -> 11.6 / 12.2 / 12.9, Qwen2.5-14B 30.4 / 29.3 / 29.8 -> 28.5 / 28.5 / 30.0.
+    // Staging the rows after the ring's first loads instead of before measured 1.4-2.5 us slower per layer.
+    const bool few = c.m >= 2 && c.m <= kFewRows && c.norm_w == nullptr;
+    const int64_t xrows = few ? c.m : 1;
+    p.spw = c.fused ? 2 : (c.m > 1 && !few && strips % 2 == 0 ? 2 : 1);
     p.groups = strips / p.spw;
-    // Staged activation bytes of a split of kts K tiles: one row, x and its group sums; several rows, rows_pad
-    // rows of x (m rounded up to a multiple of 4).
+    // Staged activation bytes of a split of kts K tiles: one or few rows, x and its group sums per row (few rows:
+    // x rounded up to whole 1 KiB transfers); several rows, rows_pad rows of x (m rounded up to a multiple of 4).
     auto stage_bytes = [&](int64_t kts) {
         const int64_t kc = kts * 128;
-        if (c.m == 1) {
-            return static_cast<size_t>(kc + 8) * 2 + static_cast<size_t>(kc / c.w.group + 1) * sizeof(float2);
+        if (c.m == 1 || few) {
+            const int64_t xst = few ? ((kc + 511) & ~int64_t{511}) + 8 : kc + 8;
+            return static_cast<size_t>(xrows) * (static_cast<size_t>(xst) * 2 + static_cast<size_t>(kc / c.w.group + 1) * sizeof(float2));
         }
         return static_cast<size_t>((c.m + 3) & ~int64_t{3}) * kc * 2;
     };
@@ -1004,10 +1064,15 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
     };
     p.wps = 1;
     p.nu = 1;
-    if (c.m == 1) {
-        // K split only to bound the staged chunk (kXBudget: 256 K tiles at one row).
+    p.few = few;
+    if (c.m == 1 || few) {
+        // K split only to bound the staged chunk (kXBudget: 256 K tiles at one row; few rows: the LDS less the
+        // largest cross-wave sums, 16 waves x 2 strips x m rows).
         const int64_t max_tiles = static_cast<int64_t>(kXBudget) / 256;
         set_splits((c.kt_count + max_tiles - 1) / max_tiles);
+        while (few && p.splits < c.kt_count && stage_bytes(p.kt_per_split) + 16 + static_cast<size_t>(16 * 2 * c.m * 16) * sizeof(float) > kLdsMax) {
+            set_splits(p.splits + 1);
+        }
         // Waves per strip group: up to 8, keeping at least 8 K tiles per wave (16 with a strip pair: measured
         // on the Llama-3-8B gate_up, 32-tile wave runs in 448 workgroups beat 16-tile runs in 896); strip
         // groups per workgroup: enough for 4 waves.
@@ -1033,7 +1098,7 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
         // unequal work (Llama-3-8B gate_up: 896 pairs in 448 workgroups of two put four pairs on 192 CUs and
         // two on the rest; seven halves on every CU: 12.72 us against 13.38 us under a kernel trace, while the down
         // GEMV that forms the split pairs takes 8.64 us against 7.79).
-        if (c.fused && c.pair_spill != nullptr && p.splits == 1 && p.wps <= 2 && c.kt_count >= 2) {
+        if (c.m == 1 && c.fused && c.pair_spill != nullptr && p.splits == 1 && p.wps <= 2 && c.kt_count >= 2) {
             const int64_t u = (2 * p.groups + cus - 1) / cus;
             if (u >= 4 && u <= 16) {
                 p.units = static_cast<int>(u);
@@ -1122,11 +1187,12 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
     }
     p.waves = p.units > 0 ? p.units : p.nu * p.wps;
     const size_t stage = stage_bytes(p.kt_per_split);
-    const size_t red = c.m == 1 ? static_cast<size_t>(p.waves) * p.spw * 16 * sizeof(float) : rows_red(p.wps, p.nu);
-    // One row: the staging, the RMSNorm's four partial sums, then the cross-wave sums; several rows: the sums
-    // reuse the staging space.
+    const bool one_math = c.m == 1 || few;
+    const size_t red = one_math ? static_cast<size_t>(p.waves) * p.spw * xrows * 16 * sizeof(float) : rows_red(p.wps, p.nu);
+    // One or few rows: the staging, the RMSNorm's four partial sums (16 bytes), then the cross-wave sums; several
+    // rows: the sums reuse the staging space.
     const size_t stage16 = (stage + 15) & ~static_cast<size_t>(15);
-    p.lds = c.m == 1 ? stage16 + 16 + red : std::max(stage16, red);
+    p.lds = one_math ? stage16 + 16 + red : std::max(stage16, red);
     if (c.m == 1 && c.pair_units > 0) { // the split's split pairs' formed columns, 32 bytes a pair
         p.lds += static_cast<size_t>(32 * (p.kt_per_split * 8 / c.pair_units + 1));
     }
@@ -1228,8 +1294,8 @@ hipError_t launch_args(const GemvArgs &a, const GemvCall &c, const GemvPlan &p, 
     const dim3 grid(static_cast<unsigned>(p.units > 0 ? (2 * p.groups + p.units - 1) / p.units : (p.groups + p.nu - 1) / p.nu), splits);
     const int group = static_cast<int>(c.w.group);
     const int ring = ring_depth(static_cast<int64_t>(grid.x) * grid.y * p.waves);
-    return c.w.dtype == 1 ? launch_dtype<F16>(a, group, c.fused, p.spw, grid, p.waves, ring, p.lds, stream)
-                          : launch_dtype<BF16>(a, group, c.fused, p.spw, grid, p.waves, ring, p.lds, stream);
+    return c.w.dtype == 1 ? launch_dtype<F16>(a, p.few, group, c.fused, p.spw, grid, p.waves, ring, p.lds, stream)
+                          : launch_dtype<BF16>(a, p.few, group, c.fused, p.spw, grid, p.waves, ring, p.lds, stream);
 }
 
 } // namespace

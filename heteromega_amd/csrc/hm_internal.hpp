@@ -97,6 +97,7 @@ struct GemvPlan {
     int64_t splits = 1, kt_per_split = 0;
     int wps = 1, nu = 1, waves = 4;
     int units = 0;
+    bool few = false; // 2..4 rows on the one-row math and launch shape (else several rows: m > 1)
     size_t lds = 0;
     size_t partial_bytes = 0;
 };

@@ -39,7 +39,7 @@ def _ffn_ref(oracle, x64, wf, dtype, channels=None):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 16])
 def test_ffn_decode_llama3_8b(oracle, hm, device, dtype, m):
     layer, _, wf = _layer(oracle, hm, device, 4096, 14336, 128, dtype, 1)
     rng = np.random.default_rng(10 + m)
@@ -323,7 +323,7 @@ def test_ffn_stack_decode_small(oracle, hm, device):
 def test_block_forward_equals_separate_ops(oracle, hm, device, dtype, hidden, inter, group, m):
     # x += FFN(RMSNorm(x) * w) in place. One row: the gate_up GEMV normalizes x while staging it and the down GEMV
     # adds its rounded output into x (two launches); other M: RMSNorm, gate_up, and a down projection that adds its
-    # rounded output into x in its epilogue (M = 2048) or in the split sum (M = 4, 16, 37, 300). Either way the bits
+    # rounded output into x in its epilogue (M = 4, 2048) or in the split sum (M = 16, 37, 300). Either way the bits
     # equal rmsnorm, forward and residual_add2 in sequence (the layer boundary of residual_norm.cu:25-98).
     layer, _, wf = _layer(oracle, hm, device, hidden, inter, group, dtype, 5)
     rng = np.random.default_rng(110 + m)

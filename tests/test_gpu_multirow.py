@@ -2,7 +2,8 @@
 the multi-row launch-shape rule's corners: narrow outputs split along K (up to 16 splits, several waves per strip
 group reducing through LDS), wide outputs with one wave per strip group, odd row counts (rows padded to a
 multiple of 4 in the staged chunk), the fused SwiGLU, and zero points up to 16 (the largest a GPTQ checkpoint
-gives after adding its one back), which the multi-row kernel takes off with the exact operand -(bias + z)."""
+gives after adding its one back), which the multi-row kernel takes off with the exact operand -(bias + z).
+Two to four rows run the one-row math with one row per lane group (their own tests below)."""
 
 import numpy as np
 import pytest
@@ -68,7 +69,7 @@ def test_multirow_fused_gate_up(oracle, hm, device, m):
 
 @pytest.mark.parametrize("m", [2, 5, 8, 16])
 @pytest.mark.parametrize("hidden,inter,group,dtype", [
-    (4096, 14336, 128, "fp16"),   # Llama-3-8B: the down GEMV splits K at every row count
+    (4096, 14336, 128, "fp16"),   # Llama-3-8B: the down GEMV splits K from 5 rows on
     (5120, 13824, 64, "bf16"),    # Qwen2.5-14B
     (2048, 8192, 128, "fp16"),    # Llama-3.2-1B
 ])
@@ -85,6 +86,27 @@ def test_forward_equals_separate_calls(oracle, hm, device, m, hidden, inter, gro
         ref = ffn.down(ffn.gate_up(x))
         torch.cuda.synchronize()
         assert torch.equal(y, ref), (m, hidden, dtype, rep)
+
+
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("k,n,g,dtype", [
+    (14336, 512, 128, "fp16"),  # the Llama-3-8B down's K: 8 waves of 14 K tiles per strip, whose rows' 1 KiB transfers overlap
+    (2688, 768, 64, "bf16"),    # 21 K tiles: each staged row rounded up to whole transfers; groups of 64
+    (3072, 1024, 32, "fp16"),   # groups of 32 (the ring sized by the kernel)
+    (28672, 128, 128, "fp16"),  # 224 K tiles: from 3 rows the staged rows exceed LDS and K splits in two
+])
+def test_few_rows_shapes(oracle, hm, device, m, k, n, g, dtype):
+    # Two to four rows: x rows staged one after another by DMA, group sums per row, lane group h of the MFMA output
+    # carrying row h; every row against float64.
+    rng = np.random.default_rng(1100 + m + k // 128 + g)
+    w_np = oracle.random_weights(rng, k, n, g, dtype)
+    w = hm.RepackedMatrix.from_logical(*logical_to_device(w_np, dtype, device), g, dtype=TORCH[dtype])
+    x64, x = make_x(oracle, rng, m, k, dtype, device)
+    y = torch.empty((m, n), dtype=TORCH[dtype], device=device)
+    print(f"few rows M={m} [{k}x{n}] g={g} {dtype}", flush=True)
+    hm.packed_linear(y, x, w)
+    torch.cuda.synchronize()
+    assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, g, dtype), dtype, f"few rows M={m} [{k}x{n}] g={g} {dtype}")
 
 
 @pytest.mark.parametrize("m", [12, 16])
