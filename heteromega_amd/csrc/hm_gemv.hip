@@ -149,9 +149,10 @@ template <class T> __device__ __forceinline__ uint4 zero_operand(uint32_t r) {
     }
 }
 
-// MT: rows the instantiation serves. 1: one row. kFewRows (2..4 rows): the one-row math and streaming with lane
-// group h of the MFMA carrying row h (A row r reads x row r / 4, so D rows 4 h .. 4 h + 3 are all row h and each
-// lane folds its element 0 as at one row: no more fold work per step than one row). 16: several rows (up to 16).
+// MT: rows the instantiation serves. 1: one row. kFewRows (2..4 rows) and 2 kFewRows (5..8 rows): the one-row math
+// and streaming with R = MT / 4 rows per lane group of the MFMA output: A row r reads x row r R / 4, so lane group h
+// holds rows R h .. R h + R - 1 (D elements 4 e / R, e < R) and folds each as one row does (R = 1: no more fold work
+// per step than one row). 16: several rows (up to 16) on the zero-point math.
 //
 // Dynamic LDS. One row: xs [kc + 8] 16-bit, sums [kc / G + 1] float2 (Xb, X), the RMSNorm's four partial sums,
 // red [waves][S][16] float, then (pair_units > 0) the formed columns of the split's split pairs, 16 per pair in
@@ -166,12 +167,14 @@ constexpr int kUnitsOut = 1, kUnitsIn = 2;
 constexpr int kFewRows = 4;
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int RING, int PAIRS = 0>
 __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) gemv_kernel(GemvArgs a) {
-    static_assert(MT == 1 || MT == kFewRows || MT == 16, "row modes");
+    static_assert(MT == 1 || MT == kFewRows || MT == 2 * kFewRows || MT == 16, "row modes");
     static_assert(PAIRS == 0 || (MT == 1 && (PAIRS == kUnitsOut ? FUSED && WGS == 1024 : !FUSED && S == 1)), "pair modes");
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr bool ONE = MT <= kFewRows;  // the one-row math (one or few rows)
-    constexpr bool FEW = MT == kFewRows;
-    constexpr int ROWS = ONE ? 1 : 4; // D elements per lane that can hold a real row
+    constexpr bool FEW = MT == kFewRows || MT == 2 * kFewRows;
+    constexpr bool ONE = MT == 1 || FEW; // the one-row math (one or few rows)
+    constexpr int RPL = FEW ? MT / 4 : 1; // rows per lane group (few rows)
+    constexpr int QE = 4 / RPL;           // D elements per row in a lane (few rows)
+    constexpr int ROWS = ONE ? RPL : 4;   // D elements per lane that can hold a real row
     constexpr int GPT = 128 / G;           // groups per strip tile
     constexpr int SPG = 4 / GPT;           // MFMA steps per group
     // Ring depth in steps: 8 tiles in flight per wave, fewer where the records (group < 128) and the
@@ -190,7 +193,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     const int tid = threadIdx.x;
     const int wave = uniform(tid >> 6);
     const int lane = tid & 63;
-    const int m = MT == 1 ? 1 : a.m; // the one-row instantiation is launched for m = 1 only, the few-row one for 2..4
+    const int m = MT == 1 ? 1 : a.m; // the one-row instantiation is launched for m = 1 only, the few-row ones for 2..4, 5..8
     const int col = lane & 15;
     const int h = lane >> 4;
 
@@ -563,10 +566,14 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
             acc[s][e] = 0.0f;
         }
     }
-    // One row: the lane's K offset in the staged row. Few rows: in row col / 4 (A rows 4 h .. 4 h + 3 are row h), and
-    // the group sums of the lane's D row h; lane groups past the last row repeat it and are not stored.
-    const uint16_t *xa = xs + (FEW ? min(col >> 2, m - 1) * xst : 0) + 8 * h;
-    const float2 *srow = sums + (FEW ? min(h, m - 1) * sst : 0);
+    // One row: the lane's K offset in the staged row. Few rows: in row col / QE (A row r is x row r / QE), and the
+    // group sums of the lane's D rows RPL h + e; rows past the last repeat it and are not stored.
+    const uint16_t *xa = xs + (FEW ? min(col / QE, m - 1) * xst : 0) + 8 * h;
+    int soff[RPL];
+#pragma unroll
+    for (int e = 0; e < RPL; ++e) {
+        soff[e] = FEW ? min(RPL * h + e, m - 1) * sst : 0;
+    }
     // Several rows: the A-operand row of this lane (rows past rows_pad read the last staged row; they only feed
     // D rows >= m, which are never stored) and its slot offsets per 32-K step; the magic of the fp16 odd pairs.
     const int arow = min(col, rows_pad - 1);
@@ -583,7 +590,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     // 10.23 -> 9.93). Issuing the next step's record permutes a step ahead as well, or forcing either ahead of the
     // step's MFMAs with a scheduling barrier, measured slower.
     uint4 xf[4];
-    float2 xg[GPT];
+    float2 xg[RPL][GPT];
     auto read_x = [&](int i) {
         const int ic = min(i, last);
 #pragma unroll
@@ -592,7 +599,10 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
 #pragma unroll
         for (int g = 0; g < GPT; ++g) {
-            xg[g] = srow[ic * GPT + g];
+#pragma unroll
+            for (int e = 0; e < RPL; ++e) {
+                xg[e][g] = sums[soff[e] + ic * GPT + g];
+            }
         }
     };
     if constexpr (ONE) {
@@ -604,14 +614,17 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         // LDS that no wave of its range staged, and NaN * 0 would survive.
         const bool live = i < te;
         uint4 av[4];
-        float2 xsum[GPT];
+        float2 xsum[RPL][GPT];
 #pragma unroll
         for (int mu = 0; mu < 4; ++mu) {
             av[mu] = xf[mu];
         }
 #pragma unroll
-        for (int g = 0; g < GPT; ++g) {
-            xsum[g] = xg[g];
+        for (int e = 0; e < RPL; ++e) {
+#pragma unroll
+            for (int g = 0; g < GPT; ++g) {
+                xsum[e][g] = xg[e][g];
+            }
         }
         uint32_t rr[S][GPT];
 #pragma unroll
@@ -639,9 +652,12 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
                 for (int s = 0; s < S; ++s) {
                     const float sc = T::to_float(rr[s][g] & 0xFFFFu);
                     const float z = static_cast<float>((rr[s][g] >> 16) & 0xFFu);
-                    const float t = __builtin_fmaf(-z, xsum[g].y, p[s][0] - xsum[g].x);
-                    const float upd = __builtin_fmaf(sc, t, acc[s][0]);
-                    acc[s][0] = live ? upd : acc[s][0];
+#pragma unroll
+                    for (int e = 0; e < RPL; ++e) {
+                        const float t = __builtin_fmaf(-z, xsum[e][g].y, p[s][QE * e] - xsum[e][g].x);
+                        const float upd = __builtin_fmaf(sc, t, acc[s][e]);
+                        acc[s][e] = live ? upd : acc[s][e];
+                    }
                 }
             }
         }
@@ -809,7 +825,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     for (int s = 0; s < S; ++s) {
 #pragma unroll
         for (int e = 0; e < ROWS; ++e) {
-            const int row = FEW ? h : 4 * h + e; // one row: lanes 0..15; few rows: lane group h holds row h
+            const int row = FEW ? RPL * h + e : 4 * h + e; // one row: lanes 0..15; few rows: lane group h holds rows RPL h + e
             if (row < m) {
                 red[((wave * S + s) * m + row) * 16 + col] = acc[s][e];
             }
@@ -944,7 +960,7 @@ hipError_t launch_w(const GemvArgs &a, dim3 grid, size_t lds, hipStream_t s, uns
 // block: threads per workgroup, WGS or (units) fewer.
 template <class T, int MT, int G, int S, bool FUSED, int WGS, int PAIRS = 0>
 hipError_t launch_r(const GemvArgs &a, dim3 grid, int ring, size_t lds, hipStream_t s, unsigned block = WGS) {
-    if constexpr (MT == kFewRows && G != 32) {
+    if constexpr ((MT == kFewRows || MT == 2 * kFewRows) && G != 32) {
         (void)ring;
         return launch_w<T, MT, G, S, FUSED, WGS, 4, PAIRS>(a, grid, lds, s, block); // 4 steps in flight
     } else if constexpr (MT == 1 && G != 32) {
@@ -1009,6 +1025,9 @@ hipError_t launch_g(const GemvArgs &a, bool fused, int strips_per_wave, dim3 gri
 
 template <class T, int MT>
 hipError_t launch_m(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
+    if constexpr (MT == 2 * kFewRows) { // groups of 128 only (the planner's rule)
+        return group == 128 ? launch_g<T, MT, 128>(a, fused, spw, grid, waves, ring, lds, s) : hipErrorInvalidConfiguration;
+    }
     switch (group) {
     case 32:
         return launch_g<T, MT, 32>(a, fused, spw, grid, waves, ring, lds, s);
@@ -1025,22 +1044,43 @@ hipError_t launch_dtype(const GemvArgs &a, bool few, int group, bool fused, int 
     if (a.m <= 1) {
         return launch_m<T, 1>(a, group, fused, spw, grid, waves, ring, lds, s);
     }
-    return few ? launch_m<T, kFewRows>(a, group, fused, spw, grid, waves, ring, lds, s)
-               : launch_m<T, 16>(a, group, fused, spw, grid, waves, ring, lds, s);
+    if (few) {
+        return a.m <= kFewRows ? launch_m<T, kFewRows>(a, group, fused, spw, grid, waves, ring, lds, s)
+                               : launch_m<T, 2 * kFewRows>(a, group, fused, spw, grid, waves, ring, lds, s);
+    }
+    return launch_m<T, 16>(a, group, fused, spw, grid, waves, ring, lds, s);
 }
 
 } // namespace
 
 namespace {
 
-GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
+GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus, bool allow_few = true) {
     GemvPlan p;
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
-    // Few rows (2..4, no RMSNorm staging): the one-row launch shape and math, the rows staged one after another
-    // (kFewRows). Against the several-row kernels, Llama-3-8B layer at M = 2 / 3 / 4: 24.1 / 24.5 / 25.0 -> 21.5 / 22.6 /
-    // 23.3 us, Llama-3.2-1B 14.4 / 14.3 / 14.7 -> 11.6 / 12.2 / 12.9, Qwen2.5-14B 30.4 / 29.3 / 29.8 -> 28.5 / 28.5 / 30.0.
+    // Few rows (no RMSNorm staging): the one-row launch shape and math, the rows staged one after another. Two to
+    // four rows always (against the several-row kernels, Llama-3-8B layer at M = 2 / 3 / 4: 24.1 / 24.5 / 25.0 ->
+    // 21.5 / 22.6 / 23.3 us, Llama-3.2-1B 14.4 / 14.3 / 14.7 -> 11.6 / 12.2 / 12.9, Qwen2.5-14B 30.4 / 29.3 / 29.8 ->
+    // 28.5 / 28.5 / 30.0). Five to eight rows (two per lane group, groups of 128) only where the several-row plan
+    // splits K and the rows fit LDS whole: the projections with K = 2048..4096 and N = 1024..6144 at M = 5 / 8
+    // 7.1-8.7 -> 5.3-6.9 / 6.3-8.3 us, the Llama-3-8B and Llama-3.2-1B downs at 5 rows 11.4 / 7.9 -> 11.3 / 6.9; a
+    // K split of the staged rows (Llama-3-8B down at 6 / 8 rows: 11.9 / 12.0 -> 14.7 / 16.2) and the large fused
+    // gate_ups that the several-row kernel runs unsplit (Llama-3-8B at 8 rows: 15.1 -> 16.4) measured slower.
     // Staging the rows after the ring's first loads instead of before measured 1.4-2.5 us slower per layer.
-    const bool few = c.m >= 2 && c.m <= kFewRows && c.norm_w == nullptr;
+    auto few_stage = [&](int64_t kts) {
+        const int64_t kc = kts * 128;
+        return static_cast<size_t>(c.m) * (static_cast<size_t>(((kc + 511) & ~int64_t{511}) + 8) * 2 +
+                                           static_cast<size_t>(kc / c.w.group + 1) * sizeof(float2));
+    };
+    const size_t few_red = static_cast<size_t>(16 * 2 * c.m * 16) * sizeof(float); // the cross-wave sums of 16 waves
+    bool few = false;
+    if (allow_few && c.m >= 2 && c.norm_w == nullptr) {
+        if (c.m <= kFewRows) {
+            few = true;
+        } else if (c.m <= 2 * kFewRows && c.w.group == 128 && few_stage(c.kt_count) + 16 + few_red <= kLdsMax) {
+            few = plan_gemv_uncached(c, cus, false).splits > 1;
+        }
+    }
     const int64_t xrows = few ? c.m : 1;
     p.spw = c.fused ? 2 : (c.m > 1 && !few && strips % 2 == 0 ? 2 : 1);
     p.groups = strips / p.spw;
@@ -1048,9 +1088,11 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
     // x rounded up to whole 1 KiB transfers); several rows, rows_pad rows of x (m rounded up to a multiple of 4).
     auto stage_bytes = [&](int64_t kts) {
         const int64_t kc = kts * 128;
-        if (c.m == 1 || few) {
-            const int64_t xst = few ? ((kc + 511) & ~int64_t{511}) + 8 : kc + 8;
-            return static_cast<size_t>(xrows) * (static_cast<size_t>(xst) * 2 + static_cast<size_t>(kc / c.w.group + 1) * sizeof(float2));
+        if (few) {
+            return few_stage(kts);
+        }
+        if (c.m == 1) {
+            return static_cast<size_t>(kc + 8) * 2 + static_cast<size_t>(kc / c.w.group + 1) * sizeof(float2);
         }
         return static_cast<size_t>((c.m + 3) & ~int64_t{3}) * kc * 2;
     };
@@ -1070,7 +1112,7 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
         // largest cross-wave sums, 16 waves x 2 strips x m rows).
         const int64_t max_tiles = static_cast<int64_t>(kXBudget) / 256;
         set_splits((c.kt_count + max_tiles - 1) / max_tiles);
-        while (few && p.splits < c.kt_count && stage_bytes(p.kt_per_split) + 16 + static_cast<size_t>(16 * 2 * c.m * 16) * sizeof(float) > kLdsMax) {
+        while (few && p.splits < c.kt_count && stage_bytes(p.kt_per_split) + 16 + few_red > kLdsMax) {
             set_splits(p.splits + 1);
         }
         // Waves per strip group: up to 8, keeping at least 8 K tiles per wave (16 with a strip pair: measured
@@ -1091,6 +1133,17 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus) {
         // Between one and two strip groups per CU (Qwen2.5-14B down: 320 strips), workgroups of twice the strips
         // run one round on fewer CUs: measured 11.2 µs against 12.1 µs for 320 workgroups.
         if (!c.fused && p.groups > cus && p.groups < 2 * cus && p.nu * p.wps <= 8) {
+            p.nu *= 2;
+        }
+        // Few rows: the staged rows bound the workgroups a CU holds; where the grid would take more than one round of
+        // them, workgroups of more strip groups share each staged chunk (Llama-3-8B down at 5..8 rows: two K splits
+        // of 256 strips in 256 workgroups of two).
+        while (few && p.nu * p.wps < 16) {
+            const size_t lds = stage_bytes(p.kt_per_split) + 16 + static_cast<size_t>(p.nu * p.wps * p.spw * c.m * 16) * sizeof(float);
+            const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(kLdsMax / lds), 16 / (p.nu * p.wps)));
+            if ((p.groups + p.nu - 1) / p.nu * p.splits <= per_cu * cus) {
+                break;
+            }
             p.nu *= 2;
         }
         // Units: given a spill for the pairs it may split, a fused call deals its (pair, K half) units evenly over

@@ -39,7 +39,7 @@ def _ffn_ref(oracle, x64, wf, dtype, channels=None):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 6, 8, 16])
 def test_ffn_decode_llama3_8b(oracle, hm, device, dtype, m):
     layer, _, wf = _layer(oracle, hm, device, 4096, 14336, 128, dtype, 1)
     rng = np.random.default_rng(10 + m)

@@ -88,16 +88,19 @@ def test_forward_equals_separate_calls(oracle, hm, device, m, hidden, inter, gro
         assert torch.equal(y, ref), (m, hidden, dtype, rep)
 
 
-@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 7, 8])
 @pytest.mark.parametrize("k,n,g,dtype", [
-    (14336, 512, 128, "fp16"),  # the Llama-3-8B down's K: 8 waves of 14 K tiles per strip, whose rows' 1 KiB transfers overlap
+    (14336, 512, 128, "fp16"),  # the Llama-3-8B down's K: 8 waves of 14 K tiles per strip, whose rows' 1 KiB transfers
+                                # overlap; up to 5 rows unsplit (150 KiB of LDS at 5)
     (2688, 768, 64, "bf16"),    # 21 K tiles: each staged row rounded up to whole transfers; groups of 64
     (3072, 1024, 32, "fp16"),   # groups of 32 (the ring sized by the kernel)
-    (28672, 128, 128, "fp16"),  # 224 K tiles: from 3 rows the staged rows exceed LDS and K splits in two
+    (28672, 128, 128, "fp16"),  # 224 K tiles: at 3 and 4 rows the staged rows exceed LDS and K splits in two
+    (4096, 2048, 128, "bf16"),  # bf16 at group 128, five to eight rows on two rows per lane group
 ])
 def test_few_rows_shapes(oracle, hm, device, m, k, n, g, dtype):
-    # Two to four rows: x rows staged one after another by DMA, group sums per row, lane group h of the MFMA output
-    # carrying row h; every row against float64.
+    # Two to four rows (any group) and, where the rows fit LDS whole, five to eight (groups of 128): x rows staged one
+    # after another by DMA, group sums per row, lane group h of the MFMA output carrying rows R h .. R h + R - 1
+    # (R = 1, 2); every row against float64. The other shapes at five to eight rows take the several-row kernel.
     rng = np.random.default_rng(1100 + m + k // 128 + g)
     w_np = oracle.random_weights(rng, k, n, g, dtype)
     w = hm.RepackedMatrix.from_logical(*logical_to_device(w_np, dtype, device), g, dtype=TORCH[dtype])
