@@ -449,9 +449,9 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     }
 
     // 1. One row: stage x into LDS (fp16: odd pairs scaled by 1/16) with the per-group sums. Consecutive lanes
-    //    take consecutive 8-element chunks, so one group is G / 8 consecutive lanes. Few rows: x is in LDS as it is
-    //    (the fp16 odd pairs' operand takes bias 64 instead, rows_operand), only row `row`'s group sums are made.
-    auto stage = [&](int row, int c8, uint4 v, uint4 g, bool valid) {
+    //    take consecutive 8-element chunks, so one group is G / 8 consecutive lanes. (Few rows: x is in LDS as it is,
+    //    the fp16 odd pairs' operand taking bias 64 instead, rows_operand; the group sums follow below.)
+    auto stage = [&](int c8, uint4 v, uint4 g, bool valid) {
         float sa = 0.0f, sb = 0.0f;
         if (norm) { // v <- round(v * scale * g) element-wise, as the RMSNorm kernel stores it
             uint32_t vw[4] = {v.x, v.y, v.z, v.w};
@@ -483,22 +483,20 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
                     }
                 }
             }
-            if constexpr (!FEW) {
-                if constexpr (T::kWide) {
-                    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-                    const h2 sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-                    v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
-                    v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
-                }
-                *reinterpret_cast<uint4 *>(xs + c8 * 8) = v;
+            if constexpr (T::kWide) {
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const h2 sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+                v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * sixteenth);
+                v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * sixteenth);
             }
+            *reinterpret_cast<uint4 *>(xs + c8 * 8) = v;
         }
         // Sum over the CPG consecutive lanes of a group with DPP (no LDS crossbar): pairs, quads, eights, sixteens.
         sa = group_sum<CPG>(sa);
         sb = group_sum<CPG>(sb);
         if (valid && (c8 % CPG) == 0) {
             const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
-            sums[row * sst + c8 / CPG] = make_float2(xb, sa + sb);
+            sums[c8 / CPG] = make_float2(xb, sa + sb);
         }
     };
     // x's chunk c8 of the split, or its formed chunk when it belongs to a split pair. pr / pu as the high word of
@@ -533,24 +531,53 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
         }
 #pragma unroll
         for (int c = 0; c < kPre; ++c) {
-            stage(0, pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]); // all lanes take part in the shuffles
+            stage(pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]); // all lanes take part in the shuffles
         }
         for (int base = kPre * 64; st_lo + base < st_hi; base += kPre * 64) {
             positions(base);
             fetch(); // long ranges only: these chunks wait behind the first ring steps
 #pragma unroll
             for (int c = 0; c < kPre; ++c) {
-                stage(0, pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]);
+                stage(pc8[c], x_chunk(pc8[c], xv[c]), wv[c], pval[c]);
             }
         }
         // The wave reads only what it wrote; LDS operations of one wave complete in order.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     } else if constexpr (FEW) {
-        for (int r = 0; r < m; ++r) {
-            for (int c8 = st_lo + lane; c8 - lane < st_hi; c8 += 64) {
-                const bool valid = c8 < st_hi;
-                const uint4 v = *reinterpret_cast<const uint4 *>(xs + r * xst + min(c8, st_hi - 1) * 8);
-                stage(r, c8, v, uint4{}, valid); // all lanes take part in the shuffles
+        // Group sums of the staged rows: one lane per (row, group) of the wave's range, adding the group's chunks in
+        // order from a lane-dependent first chunk (consecutive lanes' groups are 2 G bytes apart, so starting at
+        // chunk lane % CPG spreads one read over the banks); no shuffles. Against the one-row staging's shuffle sums
+        // over 64 chunks at a time: the Llama-3-8B down at 4 / 5 rows 10.7 / 11.4 -> 9.5 / 9.8 us, Qwen2.5-14B's at 4
+        // rows 13.7 -> 12.7, Llama-3.2-1B's 6.3 / 6.8 -> 5.7 / 5.9.
+        const int ng = (st_hi - st_lo) / CPG; // groups of the wave's range in one row
+        const int g0 = st_lo / CPG;
+        const float inv_ng = 1.0f / static_cast<float>(max(ng, 1));
+        for (int base = 0; base < m * ng; base += 64) {
+            const int idx = base + lane;
+            int r = static_cast<int>(static_cast<float>(idx) * inv_ng); // idx / ng, corrected below
+            r += (r + 1) * ng <= idx ? 1 : 0;
+            r -= r * ng > idx ? 1 : 0;
+            if (idx < m * ng) {
+                const int gi = g0 + idx - r * ng;
+                const uint16_t *src = xs + r * xst + gi * G;
+                float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+                for (int t = 0; t < CPG; ++t) {
+                    const uint4 v = *reinterpret_cast<const uint4 *>(src + ((t + lane) % CPG) * 8);
+                    if constexpr (T::kWide) {
+                        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                        const h2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+                        sa = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.z), one, __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.x), one, sa, false), false);
+                        sb = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.w), one, __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v.y), one, sb, false), false);
+                    } else {
+                        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+                        const b2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+                        sa = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, v.z), one, __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, v.x), one, sa, false), false);
+                        sb = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, v.w), one, __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, v.y), one, sb, false), false);
+                    }
+                }
+                const float xb = T::kWide ? (1024.0f * sa + 64.0f * sb) : T::kBias * (sa + sb);
+                sums[r * sst + gi] = make_float2(xb, sa + sb);
             }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1059,9 +1086,10 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus, bool allow_few = tru
     GemvPlan p;
     const int64_t strips = c.fused ? 2 * (c.n / 16) : c.n / 16;
     // Few rows (no RMSNorm staging): the one-row launch shape and math, the rows staged one after another. Two to
-    // four rows always (against the several-row kernels, Llama-3-8B layer at M = 2 / 3 / 4: 24.1 / 24.5 / 25.0 ->
-    // 21.5 / 22.6 / 23.3 us, Llama-3.2-1B 14.4 / 14.3 / 14.7 -> 11.6 / 12.2 / 12.9, Qwen2.5-14B 30.4 / 29.3 / 29.8 ->
-    // 28.5 / 28.5 / 30.0). Five to eight rows (two per lane group, groups of 128) only where the several-row plan
+    // four rows always (against the several-row kernels, with the group sums made by shuffles, Llama-3-8B layer at
+    // M = 2 / 3 / 4: 24.1 / 24.5 / 25.0 -> 21.5 / 22.6 / 23.3 us, Llama-3.2-1B 14.4 / 14.3 / 14.7 -> 11.6 / 12.2 / 12.9,
+    // Qwen2.5-14B 30.4 / 29.3 / 29.8 -> 28.5 / 28.5 / 30.0; the per-lane group sums took 0.4-1.9 us more off at 2..4
+    // rows). Five to eight rows (two per lane group, groups of 128) only where the several-row plan
     // splits K and the rows fit LDS whole: the projections with K = 2048..4096 and N = 1024..6144 at M = 5 / 8
     // 7.1-8.7 -> 5.3-6.9 / 6.3-8.3 us, the Llama-3-8B and Llama-3.2-1B downs at 5 rows 11.4 / 7.9 -> 11.3 / 6.9; a
     // K split of the staged rows (Llama-3-8B down at 6 / 8 rows: 11.9 / 12.0 -> 14.7 / 16.2) and the large fused
