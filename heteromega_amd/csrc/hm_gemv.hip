@@ -1253,18 +1253,6 @@ GemvPlan plan_gemv_uncached(const GemvCall &c, int64_t cus, bool allow_few = tru
             p.wps = 1;
             p.nu = 4;
         }
-        // A plain long-K projection of up to 4 rows with one strip per CU (3/4 of the CUs to all of them) whose whole
-        // K range fits LDS runs one strip per workgroup of 8 waves over the whole K range: no split and no partial
-        // sum, at the price of staging the whole chunk per strip (Llama-3-8B down, 256 strips, at M = 2 / 3 / 4: the
-        // layer 23.96 / 25.55 / 25.80 -> 23.11 / 24.75 / 25.20 us; Qwen2.5-14B's 320 strips would run 1.25 rounds:
-        // 29.1 -> 33.7 us at M = 2).
-        if (!c.fused && c.m <= 4 && strips >= 3 * cus / 4 && strips <= cus && c.kt_count >= 64 && stage_bytes(c.kt_count) <= kLdsMax) {
-            p.spw = 1;
-            p.groups = strips;
-            set_splits(1);
-            p.wps = 8;
-            p.nu = 1;
-        }
     }
     p.waves = p.units > 0 ? p.units : p.nu * p.wps;
     const size_t stage = stage_bytes(p.kt_per_split);
