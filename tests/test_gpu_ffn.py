@@ -112,7 +112,7 @@ def test_ffn_qwen14b_group64(oracle, hm, device):
         assert_close(oracle, host_f64(y)[sel], _ffn_ref(oracle, x64[sel], wf, "fp16"), "fp16", f"Qwen2.5-14B FFN g=64 prefill M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 1024])
+@pytest.mark.parametrize("m", [1, 3, 1024])
 def test_partition_channel_split_qwen(oracle, hm, device, m):
     # Qwen2.5-14B shape: GPU share 75% (10368 channels) and 25% (3456), run one after the other on the GPU,
     # summed, against the unsplit layer and the oracle.

@@ -60,7 +60,7 @@ def test_linear_small_groups(oracle, hm, device, group, m):
     assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, group, dtype), dtype, f"linear g={group} M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 16, 128])
+@pytest.mark.parametrize("m", [1, 3, 16, 128])
 def test_linear_prefix_and_start_column(oracle, hm, device, m):
     # leading k x n block of a larger matrix, and columns [col, col + n)
     rng = np.random.default_rng(300 + m)
