@@ -235,8 +235,8 @@ def decode_bench(hm, torch, dev, layers, m, h, steps, warmup, warm_seconds=0.0, 
     passes, warm_seconds of untimed graph replays (the clock settles) and one untimed run of the same `steps` passes.
     Eager enqueueing (6 us of host time per call) stays ahead of the GPU (20 us per pass), and its fixed cost per timed
     region is below a graph replay's (at 20 steps 20.9 against 21.3 us per pass; equal at 240). With blocks > 0 also
-    the median per pass over `blocks` event-timed replays of a graph of BLOCK passes (BASELINE's method: HIP events,
-    median). Returns (wall seconds per step, median seconds per step or None, graph of BLOCK passes, buffers)."""
+    the median per pass over `blocks` event-timed replays of a graph of BLOCK passes (the benchmark protocol's method:
+    HIP events, median). Returns (wall seconds per step, median seconds per step or None, graph of BLOCK passes, buffers)."""
     x = torch.randn((m, h), device=dev).to(layers[0].dtype)
     y = torch.empty_like(x)
     ws = layers[0].workspace(m)

@@ -1,4 +1,4 @@
-"""GPU: the BASELINE configurations that the per-layer tests do not cover at their own workload.
+"""GPU: the benchmark configurations that the per-layer tests do not cover at their own workload.
 
 - config 1: the Llama-3.2-1B FFN (H = 2048, I = 8192, g = 128) at one row, loaded from the reference's 4352-byte
   tiles, bf16 (the reference operator's type), against the float64 oracle;

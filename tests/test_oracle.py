@@ -484,7 +484,7 @@ def test_hm_gemm_emul_exact_regime_matches_float64(oracle):
 
 
 def test_cpu_baseline_llama32_1b_shape(oracle):
-    # the restated reference AVX CPU path at the Llama-3.2-1B shape (H = 2048, I = 8192, g = 128,
+    # Benchmark config 1: the restated reference AVX CPU path at the Llama-3.2-1B shape (H = 2048, I = 8192, g = 128,
     # bf16). Each GEMV as the reference checks it (test_layout_cpu.cpp:128-139: x = rand * 0.1, torch.allclose with
     # rtol 0.01, atol 0.1 against a dense matmul), then the whole decode FFN (gate, up, silu_ and mul_ in bf16,
     # down) against the float64 oracle by relative error.
