@@ -19,7 +19,7 @@
 // the whole launch: more than that only lengthens the memory queues and the launch's tail (measured on the
 // Llama-3-8B, Qwen2.5-14B and Llama-3.2-1B projections: down at 2048 waves 7.3 us with 4 steps against 7.6
 // with 8, at 2560 waves 9.8 us with 3 against 11.2 with 8, and at 1024 waves 4.6 us with 8 against 4.8
-// with 4). Two to four rows keep 4 steps.
+// with 4). Few rows keep 4 steps.
 //
 // Math per strip tile (4 MFMA steps of 32 K): the B operand is bias + q straight from the nibbles
 // (hm_device.hpp), A is the activation rows from LDS. One row:
@@ -28,13 +28,12 @@
 // and per group, with scale s and zero z of the column, sum_k x_k (q_k - z) s = s (P - Xb - z X), X = sum_k x_k.
 // Xb and X per group are computed when the wave stages x. This is the reference's per-tile factorization
 // s (sum q x - z sum x) (kernels/gpu/src/gemv_w4a16.cu:91-98, src/cpu_avx_kernels/w4a16_gemv_avx_packed.cpp:242-253),
-// applied to MFMA partial sums. Two to four rows take the same math: A row r is x row r / 4, so lane group h of the
-// MFMA output holds row h and folds it as one row does (the fp16 odd pairs' operand takes bias 64 so that the rows
-// go to LDS unscaled, by DMA, and the group sums are made from LDS). Several rows: each 32-K step runs a second
-// MFMA of the same A fragment against the constant operand -(bias + z) (the fp16 odd pairs take bias 64, so x
-// needs no scaling), so the chain holds
-// P = sum_k x_k (q_k - z) exactly in its products and the fold is one FMA s P per row: no per-group activation
-// sums, and x goes to LDS as it is, by DMA. The MFMA pipe has the room (it is idle most of the time in a
+// applied to MFMA partial sums. Two to four rows (and five to eight, two rows per lane group) take the same math: A
+// row r is x row r / 4, so lane group h of the MFMA output holds row h and folds it as one row does (the fp16 odd pairs'
+// operand takes bias 64 so that the rows go to LDS unscaled, by DMA, and the group sums are made from LDS). Several
+// rows (the rest): each 32-K step runs a second MFMA of the same A fragment against the constant operand -(bias + z)
+// (the fp16 odd pairs take bias 64, so x needs no scaling), so the chain holds P = sum_k x_k (q_k - z) exactly in its
+// products and the fold is one FMA s P per row: no per-group activation sums, and x goes to LDS as it is, by DMA. The MFMA pipe has the room (it is idle most of the time in a
 // decode GEMV); the VALU has not. One LDS read of an A fragment feeds the MFMAs of all S strips.
 //
 // Output: plain y = round(sum) (or, accumulating, y = round(y + round(sum)): a residual add), fused
