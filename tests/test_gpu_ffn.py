@@ -155,7 +155,7 @@ def test_partition_row_split_is_exact(oracle, hm, device):
     assert_close(oracle, host_f64(y), host_f64(full), "fp16", "row split 768/256")
 
 
-@pytest.mark.parametrize("m", [1, 16, 128])
+@pytest.mark.parametrize("m", [1, 3, 16, 128])
 def test_prefix_equals_separately_packed(oracle, hm, device, m):
     # Channels [0, s) of the whole layer give the bits of a layer packed from only those channels
     # (FfnSliceWeights::prefix vs pack_ffn_slice, test_gpu_ffn.cpp:472-481), and [s, I) likewise.
@@ -318,7 +318,7 @@ def test_ffn_stack_decode_small(oracle, hm, device):
         ref = host_f64(x)  # re-anchor each step so rounding flips do not compound
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 37, 300, 2048])
+@pytest.mark.parametrize("m", [1, 3, 4, 16, 37, 300, 2048])
 @pytest.mark.parametrize("dtype,hidden,inter,group", [("fp16", 4096, 14336, 128), ("bf16", 4096, 14336, 128), ("fp16", 5120, 13824, 64)])
 def test_block_forward_equals_separate_ops(oracle, hm, device, dtype, hidden, inter, group, m):
     # x += FFN(RMSNorm(x) * w) in place. One row: the gate_up GEMV normalizes x while staging it and the down GEMV

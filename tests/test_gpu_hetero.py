@@ -45,7 +45,7 @@ def test_row_and_column_splits_equal_unsplit(oracle, hm, device, gate):
         assert_close(oracle, host_f64(split)[sel], x64[sel] @ wf, "bf16", f"split {value.split_type} M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 64])
+@pytest.mark.parametrize("m", [1, 3, 64])
 def test_k_split_entry(oracle, hm, device, m):
     rng = np.random.default_rng(3)
     k0, k1, n = 7168, 7168, 4096  # a down projection split at K0 = 7168
