@@ -352,6 +352,7 @@ __global__ void __launch_bounds__(WGS) __attribute__((amdgpu_waves_per_eu(4))) g
     // i + l / 16 (column l % 16), so one coalesced load covers RB tiles (the records of consecutive tiles
     // are contiguous), and step u takes its column's record from lane 16 (u % RB) + col.
     constexpr int RB = KB < 4 ? KB : 4;
+    static_assert(KB % RB == 0, "the ring holds whole record blocks");
     const int rsub = min(lane >> 4, RB - 1);
     uint4 wq[KB][S];
     // Record blocks of the round being multiplied (rv) and of the next round (rn): a round's steps read rv
