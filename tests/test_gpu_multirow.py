@@ -112,6 +112,23 @@ def test_few_rows_shapes(oracle, hm, device, m, k, n, g, dtype):
     assert_close(oracle, host_f64(y), x64 @ oracle.weights_f64(*w_np, g, dtype), dtype, f"few rows M={m} [{k}x{n}] g={g} {dtype}")
 
 
+@pytest.mark.parametrize("m", [2, 4])
+@pytest.mark.parametrize("group,dtype", [(32, "fp16"), (64, "bf16"), (128, "bf16")])
+def test_few_rows_fused_gate_up_groups(oracle, hm, device, m, group, dtype):
+    # The few-row fused gate_up (SiLU(gate) * up from the lane's two strips, one rounding) at groups of 32 / 64 / 128 and
+    # both activation types, every output against the oracle's single-rounding SwiGLU.
+    rng = np.random.default_rng(1300 + m + group)
+    hidden, inter = 2048, 1536
+    ws = [oracle.random_weights(rng, kk, nn, group, dtype) for kk, nn in ((hidden, inter), (hidden, inter), (inter, hidden))]
+    ffn = hm.FfnLayer.from_logical(*(logical_to_device(w, dtype, device) for w in ws), group, dtype=TORCH[dtype])
+    x64, x = make_x(oracle, rng, m, hidden, dtype, device)
+    act = torch.empty((m, inter), dtype=TORCH[dtype], device=device)
+    ffn.gate_up(x, act)
+    torch.cuda.synchronize()
+    ref = oracle.silu(x64 @ oracle.weights_f64(*ws[0], group, dtype)) * (x64 @ oracle.weights_f64(*ws[1], group, dtype))
+    assert_close(oracle, host_f64(act), ref, dtype, f"few-row gate_up M={m} g={group} {dtype}")
+
+
 @pytest.mark.parametrize("m", [12, 16])
 def test_multirow_long_k_split_fallback(oracle, hm, device, m):
     # A long K at 12 or 16 rows (a Llama-3-70B down projection, K = 28672, N = 8192): the staged chunk needs at least
