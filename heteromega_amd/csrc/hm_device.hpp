@@ -29,7 +29,6 @@ constexpr int kTileBytes = 1024; // nibble bytes per strip tile
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
-typedef float float16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float bf16_bits_to_float(uint32_t b) { return __uint_as_float(b << 16); }
 
@@ -64,10 +63,6 @@ struct F16 {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
                                                        0, 0, 0);
     }
-    __device__ static __forceinline__ float16_t mfma32(uint4 a, uint4 b, float16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
-                                                       0, 0, 0);
-    }
 };
 
 struct BF16 {
@@ -78,10 +73,6 @@ struct BF16 {
     __device__ static __forceinline__ uint16_t from_float(float f) { return float_to_bf16_bits(f); }
     __device__ static __forceinline__ float4_t mfma16(uint4 a, uint4 b, float4_t c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                        c, 0, 0, 0);
-    }
-    __device__ static __forceinline__ float16_t mfma32(uint4 a, uint4 b, float16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                         c, 0, 0, 0);
     }
 };

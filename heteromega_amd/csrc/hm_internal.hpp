@@ -97,7 +97,7 @@ struct GemvPlan {
     int64_t splits = 1, kt_per_split = 0;
     int wps = 1, nu = 1, waves = 4;
     int units = 0;
-    bool few = false; // 2..4 rows on the one-row math and launch shape (else several rows: m > 1)
+    bool few = false; // 2..8 rows on the one-row math and launch shape (else several rows: m > 1)
     size_t lds = 0;
     size_t partial_bytes = 0;
 };
@@ -114,7 +114,7 @@ bool gemv_pair_supported(const GemvCall &c0, const GemvCall &c1);
 size_t gemv_pair_partial_bytes(const GemvCall &c0);
 hipError_t launch_gemv_pair(const GemvCall &c0, const GemvCall &c1, int64_t k0, hipStream_t stream);
 
-// Prefill GEMM (MFMA 32x32x16) with the same operand conventions; fused writes SiLU(gate) * up.
+// Prefill GEMM (MFMA 16x16x32) with the same operand conventions; fused writes SiLU(gate) * up.
 struct GemmCall {
     Planes w;
     const uint16_t *x = nullptr;
