@@ -1,6 +1,6 @@
 """GPU: hm_ffn_forward_static (the FFN forward on the library's static device scratch, no workspace argument)
-gives the bits of hm_ffn_forward with a caller workspace, call after call with shrinking inputs, and rejects
-requests larger than its scratch before launching anything."""
+gives the bits of hm_ffn_forward with a caller workspace, call after call with shrinking inputs (at the benchmark
+shapes and at seeded random ones), and rejects requests larger than its scratch before launching anything."""
 
 import ctypes
 
@@ -60,3 +60,32 @@ def test_static_scratch_rejects_large_requests(oracle, hm, device):
     assert _static(hm, layer, y, x, m, (0, 2048)) == hm._lib.HM_WORKSPACE_TOO_SMALL
     assert "static" in hm._lib.last_error()
     assert _static(hm, layer, y, x, 0, (0, 2048)) == hm._lib.HM_INVALID_ARGUMENT
+
+
+def test_static_scratch_random_shapes(oracle, hm, device):
+    # Seeded random layers and calls (1..16 rows, channel ranges, groups 32 / 64 / 128, both dtypes), one after
+    # another on the shared scratch: each call's bits equal hm_ffn_forward's with a caller workspace, and a call
+    # whose workspace would exceed the scratch is refused with HM_WORKSPACE_TOO_SMALL.
+    rng = np.random.default_rng(20261206)
+    lib = hm._lib.load()
+    for case in range(12):
+        group = int(rng.choice([32, 64, 128]))
+        dtype = str(rng.choice(["fp16", "bf16"]))
+        hidden = 128 * int(rng.integers(1, 26))
+        inter = 128 * int(rng.integers(1, min(49, (6 << 20) // (hidden * 128)) + 1))
+        layer = _layer(oracle, hm, device, hidden, inter, group, dtype, 100 + case)
+        for m in sorted((int(v) for v in rng.integers(1, 17, 2)), reverse=True):
+            b = 128 * int(rng.integers(0, inter // 128)) if rng.random() < 0.4 else 0
+            e = b + 128 * int(rng.integers(1, (inter - b) // 128 + 1)) if rng.random() < 0.5 else inter
+            _, x = make_x(oracle, rng, m, hidden, dtype, device)
+            y_static = torch.full((m, hidden), float("nan"), dtype=TORCH[dtype], device=device)
+            print(f"static forward case {case}: {hidden}x{inter} g={group} {dtype} m={m} channels=({b}, {e})", flush=True)
+            rc = _static(hm, layer, y_static, x, m, (b, e))
+            if lib.hm_ffn_workspace_bytes(layer._h, m) > SCRATCH_BYTES:
+                assert rc == hm._lib.HM_WORKSPACE_TOO_SMALL
+                continue
+            hm._lib.check(rc)
+            y_ws = layer.forward(x, channels=(b, e))
+            torch.cuda.synchronize()
+            assert torch.equal(y_static, y_ws), (case, m, (b, e))
+        layer.close()
