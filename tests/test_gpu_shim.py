@@ -240,6 +240,7 @@ def test_finite_check_in_reference_form(device, shim):
     assert both(False) == cols and both(True) == cols
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")  # the refused first call leaves its capture empty
 def test_repacked_copy_follows_the_tensor(oracle, hm, device, shim):
     # A repacked copy is used only while its packed tensor's storage lives unchanged: weights freed and replaced by
     # others at the same address, or rewritten in place, are repacked on the next call (not served from the old copy).
