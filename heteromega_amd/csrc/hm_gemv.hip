@@ -1052,16 +1052,17 @@ hipError_t launch_g(const GemvArgs &a, bool fused, int strips_per_wave, dim3 gri
 
 template <class T, int MT>
 hipError_t launch_m(const GemvArgs &a, int group, bool fused, int spw, dim3 grid, int waves, int ring, size_t lds, hipStream_t s) {
-    if constexpr (MT == 2 * kFewRows) { // groups of 128 only (the planner's rule)
+    if constexpr (MT == 2 * kFewRows) { // groups of 128 only (the planner's rule): no other group is instantiated
         return group == 128 ? launch_g<T, MT, 128>(a, fused, spw, grid, waves, ring, lds, s) : hipErrorInvalidConfiguration;
-    }
-    switch (group) {
-    case 32:
-        return launch_g<T, MT, 32>(a, fused, spw, grid, waves, ring, lds, s);
-    case 64:
-        return launch_g<T, MT, 64>(a, fused, spw, grid, waves, ring, lds, s);
-    default:
-        return launch_g<T, MT, 128>(a, fused, spw, grid, waves, ring, lds, s);
+    } else {
+        switch (group) {
+        case 32:
+            return launch_g<T, MT, 32>(a, fused, spw, grid, waves, ring, lds, s);
+        case 64:
+            return launch_g<T, MT, 64>(a, fused, spw, grid, waves, ring, lds, s);
+        default:
+            return launch_g<T, MT, 128>(a, fused, spw, grid, waves, ring, lds, s);
+        }
     }
 }
 
