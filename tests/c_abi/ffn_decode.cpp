@@ -1,7 +1,8 @@
 // A C++ host over the C ABI alone (include/hm_w4a16.h; no Python, no torch), as the reference's C++ model
 // integration would call it: packs a small SwiGLU FFN layer into the reference's 4352-byte tiles on the host
-// (hm_pack_w4a16), repacks it on the GPU (hm_ffn_from_tiles), runs hm_ffn_forward at M = 1 and M = 48 and
-// checks the output against a float64 evaluation of the same weights computed here. Prints PASS and exits 0
+// (hm_pack_w4a16), repacks it on the GPU (hm_ffn_from_tiles), runs hm_ffn_forward at M = 1, 3, 16 and 48 (the
+// one-row, few-row, several-row and GEMM paths) and checks the output against a float64 evaluation of the same
+// weights computed here. Prints PASS and exits 0
 // on success; exits 2 when no GPU is visible.
 #include "hm_w4a16.h"
 
@@ -114,7 +115,7 @@ int main() {
     CHECK_HIP(hipMalloc(&dy, static_cast<size_t>(MaxM) * H * 2));
 
     std::normal_distribution<float> normal(0.0f, 1.0f);
-    for (const int M : {1, MaxM}) {
+    for (const int M : {1, 3, 16, MaxM}) {
         std::vector<uint16_t> x(static_cast<size_t>(M) * H), y(x.size());
         for (auto &v : x) v = bf16_bits(normal(rng));
         CHECK_HIP(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice));

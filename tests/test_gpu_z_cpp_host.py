@@ -1,6 +1,6 @@
 """GPU: a C++ host over the C ABI alone (tests/c_abi/ffn_decode.cpp, built by __graft_entry__.build()): host
-packing to 4352-byte tiles, device repack and hm_ffn_forward at M = 1 and 48, checked in the program against
-a float64 evaluation of the same weights."""
+packing to 4352-byte tiles, device repack and hm_ffn_forward at M = 1, 3, 16 and 48, checked in the program
+against a float64 evaluation of the same weights."""
 
 import os
 import subprocess
