@@ -38,16 +38,21 @@ typedef enum hm_status {
     HM_WORKSPACE_TOO_SMALL = 5
 } hm_status;
 
+/* The *_FORCE_INT32_ enumerators are no values: they make each enumeration span every 32-bit value, so that a value
+ * outside the list that a caller passes is still a value of the type in C++ and the library rejects it with
+ * HM_INVALID_ARGUMENT (C++ gives an enumeration without them only the values of its enumerators' bit width). */
 typedef enum hm_dtype {
     HM_BF16 = 0, /* reference surface: include/hipkernels/w4a16_gemm_packed.hpp:31-33 */
-    HM_FP16 = 1
+    HM_FP16 = 1,
+    HM_DTYPE_FORCE_INT32_ = -2147483647 - 1
 } hm_dtype;
 
 /* Column order of a reference-packed gate_up matrix
  * (kernels/gpu/include/heteromega/gpu_ffn.hpp:43-46). */
 typedef enum hm_gate_up_layout {
-    HM_GATE_UP_BLOCKED = 0,    /* [gate 0..n) | up 0..n) ] */
-    HM_GATE_UP_INTERLEAVED = 1 /* per 64 channels: 64 gate columns, then 64 up columns */
+    HM_GATE_UP_BLOCKED = 0,     /* [gate 0..n) | up 0..n) ] */
+    HM_GATE_UP_INTERLEAVED = 1, /* per 64 channels: 64 gate columns, then 64 up columns */
+    HM_GATE_UP_LAYOUT_FORCE_INT32_ = -2147483647 - 1
 } hm_gate_up_layout;
 
 int hm_abi_version(void);
