@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <new>
 #include <mutex>
 #include <string>
 
@@ -31,12 +32,11 @@ struct hm_ffn {
 
 namespace {
 
-thread_local std::string g_error;
+// The last error message of this thread: a fixed buffer, so that reporting an error allocates nothing.
+thread_local char g_error[512];
 
 hm_status vfail(hm_status s, const char *fmt, va_list ap) {
-    char buf[512];
-    std::vsnprintf(buf, sizeof(buf), fmt, ap);
-    g_error = buf;
+    std::vsnprintf(g_error, sizeof(g_error), fmt, ap);
     return s;
 }
 
@@ -312,7 +312,10 @@ void destroy_ffn(hm_ffn *f) {
 
 // An FFN layer with both planes allocated (gate_up [H, 2 I] fused, down [I, H]).
 hm_status new_ffn(int64_t hidden, int64_t inter, int64_t group, hm_dtype dtype, hm_ffn **out) {
-    auto *f = new hm_ffn;
+    auto *f = new (std::nothrow) hm_ffn;
+    if (f == nullptr) {
+        return fail(HM_OUT_OF_MEMORY, "host allocation of a layer handle failed");
+    }
     f->hidden = hidden;
     f->inter = inter;
     hm_status st = alloc_planes(&f->gate_up, hidden, 2 * inter, group, dtype);
@@ -414,7 +417,7 @@ extern "C" {
 
 int hm_abi_version(void) { return HM_ABI_VERSION; }
 
-const char *hm_last_error(void) { return g_error.c_str(); }
+const char *hm_last_error(void) { return g_error; }
 
 int64_t hm_packed_bytes(int64_t K, int64_t N) {
     if (K <= 0 || N <= 0 || K % 128 || N % 64) {
@@ -525,7 +528,10 @@ hm_status hm_weights_from_tiles(const uint8_t *tiles, int64_t packed_k, int64_t 
     if (st != HM_OK || (st = check_tile_source(tiles, packed_k, packed_n, K, N, "hm_weights_from_tiles")) != HM_OK) {
         return st;
     }
-    auto *w = new hm_weights;
+    auto *w = new (std::nothrow) hm_weights;
+    if (w == nullptr) {
+        return fail(HM_OUT_OF_MEMORY, "host allocation of a weights handle failed");
+    }
     if ((st = alloc_planes(w, K, N, 128, dtype)) != HM_OK) {
         delete w;
         return st;
@@ -559,7 +565,10 @@ hm_status hm_weights_from_logical(const uint8_t *q, const uint16_t *scales, cons
     if (st != HM_OK || (st = check_logical(q, scales, zeros, K, N, group, "hm_weights_from_logical")) != HM_OK) {
         return st;
     }
-    auto *w = new hm_weights;
+    auto *w = new (std::nothrow) hm_weights;
+    if (w == nullptr) {
+        return fail(HM_OUT_OF_MEMORY, "host allocation of a weights handle failed");
+    }
     if ((st = alloc_planes(w, K, N, group, dtype)) != HM_OK) {
         delete w;
         return st;
@@ -594,7 +603,10 @@ hm_status hm_weights_from_gate_up_tiles(const uint8_t *gate_up, int64_t packed_k
     if (st != HM_OK || (st = check_gate_up_source(gate_up, packed_k, stored, K, channels, layout, "hm_weights_from_gate_up_tiles")) != HM_OK) {
         return st;
     }
-    auto *w = new hm_weights;
+    auto *w = new (std::nothrow) hm_weights;
+    if (w == nullptr) {
+        return fail(HM_OUT_OF_MEMORY, "host allocation of a weights handle failed");
+    }
     if ((st = alloc_planes(w, K, 2 * channels, 128, dtype)) != HM_OK) {
         delete w;
         return st;
@@ -694,7 +706,10 @@ hm_status hm_weights_concat(const hm_weights *const *parts, int32_t count, void 
         }
         n += w->p.N;
     }
-    auto *c = new hm_weights;
+    auto *c = new (std::nothrow) hm_weights;
+    if (c == nullptr) {
+        return fail(HM_OUT_OF_MEMORY, "host allocation of a weights handle failed");
+    }
     hm_status st = alloc_planes(c, parts[0]->p.K, n, parts[0]->p.group, parts[0]->p.dtype);
     if (st != HM_OK) {
         delete c;

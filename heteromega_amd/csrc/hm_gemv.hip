@@ -46,6 +46,7 @@
 #include <array>
 #include <cmath>
 #include <cstdlib>
+#include <exception>
 #include <unordered_map>
 
 namespace hm {
@@ -1310,7 +1311,11 @@ GemvPlan plan_gemv(const GemvCall &c) {
         cache.clear();
     }
     const GemvPlan p = plan_gemv_uncached(c, cus);
-    cache.emplace(key, p);
+    try {
+        cache.emplace(key, p);
+    } catch (const std::exception &) {
+        // a failed host allocation only leaves the plan uncached
+    }
     return p;
 }
 

@@ -11,9 +11,11 @@
 #include <array>
 #include <cstdint>
 #include <cstring>
+#include <exception>
 #include <limits>
 #include <map>
 #include <mutex>
+#include <new>
 
 struct hm_split_table {
     std::map<std::array<int32_t, 5>, hm_split_desc> entries;
@@ -125,12 +127,27 @@ int32_t hm_layer_id(const char *layer_type) {
     return 0;
 }
 
+namespace {
+
+// Inserts or replaces an entry; false when the host allocation fails (no exception leaves the C ABI).
+bool store(hm_split_table *t, const std::array<int32_t, 5> &key, const hm_split_desc &d) {
+    try {
+        std::lock_guard<std::mutex> lock(t->mu);
+        t->entries[key] = d;
+        return true;
+    } catch (const std::exception &) {
+        return false;
+    }
+}
+
+} // namespace
+
 hm_status hm_split_table_create(hm_split_table **out) {
     if (out == nullptr) {
         return hm::set_error(HM_INVALID_ARGUMENT, "hm_split_table_create: null output handle");
     }
-    *out = new hm_split_table;
-    return HM_OK;
+    *out = new (std::nothrow) hm_split_table;
+    return *out != nullptr ? HM_OK : hm::set_error(HM_OUT_OF_MEMORY, "hm_split_table_create: host allocation failed");
 }
 
 hm_status hm_split_table_destroy(hm_split_table *t) {
@@ -160,8 +177,9 @@ hm_status hm_split_table_add_gemm(hm_split_table *t, int32_t forM, int32_t forK,
     if (npuM == 0) {
         return HM_OK; // GPU-only in the reference: the loader skips it (npuSetup.cpp:1312-1319)
     }
-    std::lock_guard<std::mutex> lock(t->mu);
-    t->entries[{forM, forK, forN, layer_id, chunk_id}] = make_desc(npuM, npuK, npuN, 0, 1, config, split);
+    if (!store(t, {forM, forK, forN, layer_id, chunk_id}, make_desc(npuM, npuK, npuN, 0, 1, config, split))) {
+        return hm::set_error(HM_OUT_OF_MEMORY, "hm_split_table_add_gemm: host allocation failed");
+    }
     if (stored != nullptr) {
         *stored = 1;
     }
@@ -177,8 +195,9 @@ hm_status hm_split_table_add_gemv(hm_split_table *t, int32_t forK, int32_t forN,
         return hm::set_error(HM_INVALID_ARGUMENT, "hm_split_table_add_gemv: forK %d, forN %d must be positive, npuN %d, cpuN %d, cpuThreads %d not negative",
                              forK, forN, npuN, cpuN, cpuThreads);
     }
-    std::lock_guard<std::mutex> lock(t->mu);
-    t->entries[{1, forK, forN, layer_id, chunk_id}] = make_desc(1, forK, npuN, cpuN, cpuThreads, config, 0);
+    if (!store(t, {1, forK, forN, layer_id, chunk_id}, make_desc(1, forK, npuN, cpuN, cpuThreads, config, 0))) {
+        return hm::set_error(HM_OUT_OF_MEMORY, "hm_split_table_add_gemv: host allocation failed");
+    }
     return HM_OK;
 }
 
